@@ -1,0 +1,224 @@
+/* mc_kv.h - C ABI of the paged KV-cache hot path in libminicpm_native.so
+ * (MI355X / gfx950 build).
+ *
+ * These entry points are the plain-pointer equivalents of the reference's
+ * internal launcher boundary (native/kernels/sm120/kernels.h) and of its
+ * PagedKvAllocator (native/runtime/kv_cache.h:68-104). Each declaration cites
+ * the reference interface it replaces. Conventions kept from the reference:
+ *   - bf16 values travel as uint16_t bit patterns;
+ *   - positions / decode limits are read from a DEVICE address at kernel run
+ *     time (so a captured graph replays with new positions);
+ *   - argument checks return MC_E_INVALID_ARGUMENT, launch failures MC_E_CUDA,
+ *     and set the thread-local message returned by mc_last_error();
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *
+ * Model geometry is fixed as in the reference (generated_model_config.h):
+ * 16 query heads, 2 KV heads (GQA group 8), head_dim 128. A qkv row is 2560
+ * bf16: q in columns 0..2047, k in 2048..2303, v in 2304..2559.
+ *
+ * Pool layout (reference kv_cache.h:29-66 with the page size as a parameter):
+ *   element offset = (((layer*max_pages + page)*P + slot)*512 + kv*256
+ *                     + head*128 + d)           (bf16 elements)
+ *   pos -> page = page_table[pos / P], slot = pos % P.
+ */
+#ifndef MC_KV_H_
+#define MC_KV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "minicpm_runtime.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Exported even when the library is built with -fvisibility=hidden. */
+#pragma GCC visibility push(default)
+
+#define MC_KV_Q_HEADS 16u
+#define MC_KV_KV_HEADS 2u
+#define MC_KV_HEAD_DIM 128u
+#define MC_KV_QKV_ROW 2560u
+#define MC_KV_PARTIAL_STRIDE 130u /* {m, l, acc[128]} fp32 (kernels.h:277) */
+#define MC_KV_MERGE_SPLIT2 32u    /* level-2 merge splits (kernels.h:283) */
+
+/* Pool geometry passed by value. The reference fixes tokens_per_page = 32 and
+ * num_layers = 42 at compile time (kv_cache.h:30, :63-65); here both are
+ * runtime values. tokens_per_page must be a power of two in [1, 4096]. */
+typedef struct mc_kv_layout_t {
+    uint32_t max_pages;       /* pages per layer */
+    uint32_t tokens_per_page; /* P */
+    uint32_t num_layers;      /* L */
+    uint32_t reserved;        /* must be 0 */
+} mc_kv_layout_t;
+
+/* ---- addressing (host-only, integer) ---- */
+
+/* KvLayout::elem_offset (kv_cache.h:40-45). Returns UINT64_MAX on a bad layout. */
+uint64_t mc_kv_elem_offset(mc_kv_layout_t layout, uint32_t layer, uint32_t page,
+                           uint32_t slot, uint32_t kv, uint32_t head, uint32_t d);
+/* KvLayout::total_elems (kv_cache.h:60-65): max_pages*P*512*num_layers. */
+uint64_t mc_kv_total_elems(mc_kv_layout_t layout);
+/* attention_decode_chunk_pos tier table (kernels.h:295-304, 512 tier off). */
+uint32_t mc_kv_decode_chunk_pos(uint32_t max_ctx);
+/* attention_decode_max_chunks (kernels.h:308-311). */
+uint32_t mc_kv_decode_max_chunks(uint32_t max_ctx, uint32_t chunk_pos);
+/* prefill_flash_split_kv (kernels.h:517-521). */
+uint32_t mc_kv_prefill_split_kv(uint32_t tokens);
+
+/* ---- per-session page allocator (PagedKvAllocator, kv_cache.cpp:8-91) ---- */
+typedef struct mc_kv_allocator mc_kv_allocator_t;
+
+/* PagedKvAllocator::init: d_table is a device u32[max_pages]. */
+mc_status_t mc_kv_allocator_create(uint32_t* d_table, uint32_t max_pages,
+                                   uint32_t tokens_per_page,
+                                   mc_kv_allocator_t** out);
+void mc_kv_allocator_destroy(mc_kv_allocator_t* a);
+/* PagedKvAllocator::ensure_pages_for: lowest-free-page growth to
+ * ceil(total_tokens/P) pages; H2D of the table prefix only when it grew;
+ * MC_E_OUT_OF_MEMORY when the pool is too small. */
+mc_status_t mc_kv_allocator_ensure_pages_for(mc_kv_allocator_t* a,
+                                             uint32_t total_tokens, void* stream);
+/* PagedKvAllocator::release_all: clears ownership, keeps device table. */
+void mc_kv_allocator_release_all(mc_kv_allocator_t* a);
+uint32_t mc_kv_allocator_pages_owned(const mc_kv_allocator_t* a);
+uint32_t mc_kv_allocator_pages_synced(const mc_kv_allocator_t* a);
+/* Copies min(n, pages_owned) entries of the host shadow table. */
+uint32_t mc_kv_allocator_host_table(const mc_kv_allocator_t* a, uint32_t* out,
+                                    uint32_t n);
+
+/* ---- shared page pool (several sessions in one pool; per-session free) ----
+ * No reference counterpart: the reference gives each session a private pool
+ * (session.cpp:227-231). This pool serves the interleaved batched-decode and
+ * churn workloads. Allocation takes the lowest free page id (same rule as
+ * PagedKvAllocator::first_free_page, kv_cache.cpp:24-36); a session's pages
+ * are returned by mc_kv_pool_release and become reusable. */
+typedef struct mc_kv_pool mc_kv_pool_t;
+
+mc_status_t mc_kv_pool_create(uint32_t max_pages, uint32_t tokens_per_page,
+                              uint32_t max_sessions, mc_kv_pool_t** out);
+void mc_kv_pool_destroy(mc_kv_pool_t* p);
+/* Grows session `sid` to cover total_tokens; appends new page ids to its host
+ * table and, if d_table != NULL and the table grew, uploads the grown suffix
+ * to d_table (device u32[max pages per session]) on `stream`. */
+mc_status_t mc_kv_pool_ensure(mc_kv_pool_t* p, uint32_t sid,
+                              uint32_t total_tokens, uint32_t* d_table,
+                              void* stream);
+/* Frees every page of session `sid`. */
+mc_status_t mc_kv_pool_release(mc_kv_pool_t* p, uint32_t sid);
+uint32_t mc_kv_pool_pages_free(const mc_kv_pool_t* p);
+uint32_t mc_kv_pool_session_pages(const mc_kv_pool_t* p, uint32_t sid);
+uint32_t mc_kv_pool_session_table(const mc_kv_pool_t* p, uint32_t sid,
+                                  uint32_t* out, uint32_t n);
+
+/* ---- RoPE + K/V append ---- */
+
+/* launch_rope_inv_freq_init (kernels.h:229-230, rope_kv.cu:104-124):
+ * d_table[p] = (float)pow(theta, -p/64), p < 64. */
+mc_status_t mc_kv_rope_inv_freq_init(float* d_table, double rope_theta,
+                                     void* stream);
+
+/* launch_rope_kv (kernels.h:214-225, rope_kv.cu:30-96,126-148): for token t
+ * at pos = *d_base_pos + t, rotate q (in place, 16 heads), rotate k and store
+ * it to the pool (kv=0), copy v to the pool (kv=1). d_inv_freq may be NULL
+ * (then computed from rope_theta in the kernel). */
+mc_status_t mc_kv_rope_append(uint16_t* d_qkv, uint32_t tokens,
+                              const uint32_t* d_base_pos, uint32_t layer,
+                              const uint32_t* d_page_table, uint16_t* d_kv_pool,
+                              mc_kv_layout_t layout, double rope_theta,
+                              const float* d_inv_freq, void* stream);
+
+/* ---- decode attention (split-KV flash decoding) ---- */
+
+/* launch_attention_decode (kernels.h:369-388, attention_decode.cu:1840-1964).
+ * Attends positions 0..limit (limit = *d_pos) of one session. Chunk kernel
+ * writes partials [16][max_chunks][130]; if limit < chunk_pos it writes
+ * d_out [2048] directly. d_partials2 != NULL selects the two-level merge
+ * (level-2 partials [16][32][130]); NULL selects the one-level merge.
+ * d_inv_freq != NULL enables phase0: q and k of position `limit` are rotated
+ * from d_q_rows, K/V of `limit` are written to the pool (pool may be written
+ * only in that case). chunk_pos must be a multiple of 16. */
+mc_status_t mc_kv_attention_decode(const uint16_t* d_q_rows, const uint32_t* d_pos,
+                                   uint32_t layer, const uint32_t* d_page_table,
+                                   uint16_t* d_kv_pool, mc_kv_layout_t layout,
+                                   float* d_partials, uint32_t max_chunks,
+                                   uint16_t* d_out, void* stream,
+                                   const float* d_inv_freq, uint32_t chunk_pos,
+                                   float* d_partials2);
+
+/* launch_attention_decode_merge (kernels.h:394-400): merge only, from given
+ * level-1 partials. */
+mc_status_t mc_kv_attention_decode_merge(const float* d_partials,
+                                         const uint32_t* d_pos,
+                                         uint32_t max_chunks, uint32_t chunk_pos,
+                                         float* d_partials2, uint16_t* d_out,
+                                         void* stream);
+
+/* Chunk kernel only (no merge): the test/bench twin of launch_attn_kv_h_test
+ * (kernels.h:441-450) without the score scratch. */
+mc_status_t mc_kv_attention_decode_chunks(const uint16_t* d_q_rows,
+                                          const uint32_t* d_pos, uint32_t layer,
+                                          const uint32_t* d_page_table,
+                                          uint16_t* d_kv_pool,
+                                          mc_kv_layout_t layout,
+                                          float* d_partials, uint32_t max_chunks,
+                                          uint16_t* d_out, void* stream,
+                                          const float* d_inv_freq,
+                                          uint32_t chunk_pos);
+
+/* launch_attention_decode_batch (kernels.h:465-480,
+ * attention_decode.cu:2120-2170). Slot s uses q row d_q_rows + s*2560,
+ * limit *d_slot_pos[s], page table d_slot_pt[s], pool d_slot_kv[s]; writes
+ * d_partials + s*16*max_chunks*130, d_partials2 + s*16*32*130 and
+ * d_out + s*2048. Results are bit-identical to B single-session calls. The
+ * three pointer tables live in device memory. */
+mc_status_t mc_kv_attention_decode_batch(const uint16_t* d_q_rows,
+                                         const uint32_t* const* d_slot_pos,
+                                         uint32_t B, uint32_t layer,
+                                         const uint32_t* const* d_slot_pt,
+                                         uint16_t* const* d_slot_kv,
+                                         mc_kv_layout_t layout, float* d_partials,
+                                         uint32_t max_chunks, uint16_t* d_out,
+                                         void* stream, const float* d_inv_freq,
+                                         uint32_t chunk_pos, float* d_partials2);
+
+/* ---- prefill attention over the paged cache ---- */
+
+/* launch_attn_prefill_flash (kernels.h:575-585, attention_prefill.cu:291-729):
+ * causal attention of T query rows (absolute positions *d_base_pos + t) over
+ * pool positions 0..*d_base_pos + t gathered through the page table.
+ * S_kv in 1..8 key splits; S_kv > 1 needs d_partials of
+ * T*16*S_kv*130 floats and runs the split merge. Writes d_out [T][2048]. */
+mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_t tokens,
+                                    const uint32_t* d_base_pos, uint32_t layer,
+                                    const uint32_t* d_page_table,
+                                    const uint16_t* d_kv_pool,
+                                    mc_kv_layout_t layout, uint16_t* d_out,
+                                    float* d_partials, uint32_t S_kv,
+                                    void* stream);
+
+/* ---- device-side sequence advance ---- */
+
+/* launch_decode_advance (kernels.h:632-635, sampling.cu:58-67):
+ * d_seq[*d_seq_len] = *d_next_token; *d_seq_len += 1. */
+mc_status_t mc_kv_decode_advance(int32_t* d_seq, const int32_t* d_next_token,
+                                 uint32_t* d_seq_len, void* stream);
+
+/* launch_batch_advance (kernels.h:651-655, sampling.cu:241-251): per slot s,
+ * d_slot_seq[s][*d_slot_pos[s]] = *d_slot_tok[s]; *d_slot_pos[s] += 1. */
+mc_status_t mc_kv_batch_advance(int32_t* const* d_slot_seq,
+                                const int32_t* const* d_slot_tok,
+                                uint32_t* const* d_slot_pos, uint32_t n,
+                                void* stream);
+
+/* Library build identity, e.g. "minicpm-kv gfx950". */
+const char* mc_kv_build_info(void);
+
+#pragma GCC visibility pop
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* MC_KV_H_ */
