@@ -1,0 +1,350 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged KV-cache hot path.
+
+Metric: decode-attention us/layer and KV HBM GB/s (% of peak) at
+2K, 8x2K batch and 128K. One "step" = one decode step of the 28-layer stack at
+the headline workload C4 (one session, 131072 cached tokens in 2048 pages of
+64, chunk 256, two-level merge): per layer the fused append+attend decode
+(phase0) over that layer's pool slice. `value` is the K+V bytes attended per
+second over the whole timed region (inputs resident in HBM); the other
+configurations are reported under "configs".
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+LAYERS = 28
+P = 64
+KV_BYTES_PER_TOKEN = 1024  # K+V, 2 kv heads x 128 dims x bf16, one layer
+QO_BYTES = 16 * 128 * 2 * 2  # q read + out write per session
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="c4,c3,c1,c2")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true", help="no HIP graphs (eager launches)")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on torch's current stream (the stream every launch uses).
+
+    Each workload step is captured once into a HIP graph (torch.cuda.CUDAGraph)
+    and replayed, so the timed region measures the GPU and not Python launch
+    overhead; the kernels read positions from device memory, so replays are
+    exact re-executions."""
+
+    def __init__(self, torch, graphs=True):
+        self.torch = torch
+        self.graphs = graphs
+
+    def capture(self, fns):
+        """Returns a callable cycling through `fns` (one per rotation index),
+        each captured into its own graph when graphs are enabled."""
+        t = self.torch
+        if not self.graphs:
+            state = {"i": 0}
+
+            def eager():
+                fns[state["i"] % len(fns)]()
+                state["i"] += 1
+            return eager
+        for f in fns:  # eager warm-up outside capture
+            f()
+        t.cuda.synchronize()
+        gs = []
+        for f in fns:
+            g = t.cuda.CUDAGraph()
+            with t.cuda.graph(g):
+                f()
+            gs.append(g)
+        t.cuda.synchronize()
+        state = {"i": 0}
+
+        def replay():
+            gs[state["i"] % len(gs)].replay()
+            state["i"] += 1
+        replay.graphs = gs
+        return replay
+
+    def run(self, fn, reps):
+        t = self.torch
+        t.cuda.synchronize()
+        a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        t.cuda.synchronize()
+        return a.elapsed_time(b) / reps  # ms
+
+
+def make_session_pool(torch, dev, n_pages_total, layers):
+    """bf16 pool of `layers` layers, values ~N(0,1)/sqrt(128) (bf16 bits as int16)."""
+    elems = n_pages_total * P * 512 * layers
+    x = torch.empty(elems, dtype=torch.bfloat16, device=dev)
+    x.normal_(0.0, 1.0 / 128 ** 0.5)
+    return x.view(torch.int16)
+
+
+def q_rows(torch, dev, n):
+    x = torch.empty(n * 2560, dtype=torch.bfloat16, device=dev)
+    x.normal_(0.0, 1.0 / 128 ** 0.5)
+    return x.view(torch.int16)
+
+
+def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
+    """One session, `ctx` cached tokens incl. the appended one; `rot` pool copies
+    rotated per step so the working set exceeds the 256 MB Infinity Cache."""
+    npages = ctx // P
+    maxp = npages
+    lay = kvm.KvLayout(maxp, P, LAYERS)
+    C = kvm.attention_decode_chunk_pos(ctx)
+    NC = kvm.attention_decode_max_chunks(ctx, C)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    pt = torch.randperm(maxp, generator=g).to(torch.int32).to(dev)
+    pools = [make_session_pool(torch, dev, maxp, LAYERS) for _ in range(rot)]
+    qs = q_rows(torch, dev, LAYERS)
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    inv = torch.empty(64, dtype=torch.float32, device=dev)
+    kvm.launch_rope_inv_freq_init(inv, 5e6)
+    parts = torch.empty(16 * NC * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.empty(16 * 32 * 130, dtype=torch.float32, device=dev)
+    out = torch.empty(LAYERS * 2048, dtype=torch.int16, device=dev)
+    def step_on(pool):
+        def f():
+            for l in range(LAYERS):
+                kvm.launch_attention_decode(qs[l * 2560:], pos, l, pt, pool, lay, parts,
+                                            NC, out[l * 2048:], d_inv_freq=inv,
+                                            chunk_pos=C, d_partials2=parts2)
+        return f
+
+    def chunks_on(pool):
+        def f():
+            for l in range(LAYERS):
+                kvm.launch_attention_decode_chunks(qs[l * 2560:], pos, l, pt, pool, lay,
+                                                   parts, NC, out[l * 2048:],
+                                                   d_inv_freq=inv, chunk_pos=C)
+        return f
+
+    step = timer.capture([step_on(p) for p in pools])
+    chunks_only = timer.capture([chunks_on(p) for p in pools])
+    timer.run(step, warmup)
+    ms = timer.run(step, steps)
+    timer.run(chunks_only, max(1, warmup))
+    ms_chunk = timer.run(chunks_only, steps)
+    bytes_layer = ctx * KV_BYTES_PER_TOKEN + QO_BYTES
+    del pools
+    return {
+        "ctx": ctx, "sessions": 1, "chunk_pos": C, "pages_per_layer": npages,
+        "ms_per_step": ms, "us_per_layer": ms * 1e3 / LAYERS,
+        "kv_gbs": bytes_layer * LAYERS / (ms * 1e-3) / 1e9,
+        "pct_hbm_peak": 100.0 * bytes_layer * LAYERS / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "tokens_per_s": 1e3 / ms,
+        "chunk_kernel_us": ms_chunk * 1e3 / LAYERS,
+        "chunk_kernel_gbs": bytes_layer / (ms_chunk * 1e-3 / LAYERS) / 1e9,
+        "algorithmic_bytes_per_layer": bytes_layer,
+        "pool_copies_rotated": rot,
+    }
+
+
+def bench_decode_batch(kvm, torch, dev, timer, B, ctx, steps, warmup):
+    """B sessions in one shared pool, pages interleaved by a seeded shuffle;
+    each step appends one token per session (phase0) and attends."""
+    pages_per = ctx // P
+    maxp = pages_per * B
+    lay = kvm.KvLayout(maxp, P, LAYERS)
+    C = kvm.attention_decode_chunk_pos(ctx)
+    NC = kvm.attention_decode_max_chunks(ctx, C)
+    g = torch.Generator(device="cpu").manual_seed(3)
+    perm = torch.randperm(maxp, generator=g).to(torch.int32)
+    pts = [perm[s::B].contiguous().to(dev) for s in range(B)]
+    pool = make_session_pool(torch, dev, maxp, LAYERS)
+    qs = q_rows(torch, dev, LAYERS * B)
+    lims = [torch.tensor([ctx - 1], dtype=torch.int32, device=dev) for _ in range(B)]
+    tab = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
+    d_pos, d_pt, d_kv = tab(lims), tab(pts), tab([pool] * B)
+    inv = torch.empty(64, dtype=torch.float32, device=dev)
+    kvm.launch_rope_inv_freq_init(inv, 5e6)
+    parts = torch.empty(B * 16 * NC * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.empty(B * 16 * 32 * 130, dtype=torch.float32, device=dev)
+    out = torch.empty(B * 2048, dtype=torch.int16, device=dev)
+
+    def step_f():
+        for l in range(LAYERS):
+            kvm.launch_attention_decode_batch(qs[l * B * 2560:], d_pos, B, l, d_pt, d_kv, lay,
+                                              parts, NC, out, d_inv_freq=inv, chunk_pos=C,
+                                              d_partials2=parts2)
+
+    step = timer.capture([step_f])
+    timer.run(step, warmup)
+    ms = timer.run(step, steps)
+    bytes_layer = B * (ctx * KV_BYTES_PER_TOKEN + QO_BYTES)
+    return {
+        "ctx": ctx, "sessions": B, "chunk_pos": C, "ms_per_step": ms,
+        "us_per_layer": ms * 1e3 / LAYERS,
+        "kv_gbs": bytes_layer * LAYERS / (ms * 1e-3) / 1e9,
+        "pct_hbm_peak": 100.0 * bytes_layer * LAYERS / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "tokens_per_s": B * 1e3 / ms,
+        "algorithmic_bytes_per_layer": bytes_layer,
+    }
+
+
+def bench_append(kvm, torch, dev, timer, T, steps, warmup):
+    """C2: RoPE + K/V append of one 8448-token prefill chunk for 28 layers."""
+    npages = T // P
+    maxp = npages
+    lay = kvm.KvLayout(maxp, P, LAYERS)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    pt = torch.randperm(maxp, generator=g).to(torch.int32).to(dev)
+    pool = torch.zeros(maxp * P * 512 * LAYERS, dtype=torch.int16, device=dev)
+    qkv = q_rows(torch, dev, T * LAYERS)
+    base = torch.zeros(1, dtype=torch.int32, device=dev)
+    inv = torch.empty(64, dtype=torch.float32, device=dev)
+    kvm.launch_rope_inv_freq_init(inv, 1e4)
+
+    def step_f():
+        for l in range(LAYERS):
+            kvm.launch_rope_kv(qkv[l * T * 2560:], T, base, l, pt, pool, lay, 1e4,
+                               d_inv_freq=inv)
+
+    step = timer.capture([step_f])
+    timer.run(step, warmup)
+    ms = timer.run(step, steps)
+    kv_bytes = T * 512 * 2 * 2  # k,v read + page write
+    q_bytes = T * 2048 * 2 * 2  # q read + write (rotated in place)
+    us = ms * 1e3 / LAYERS
+    return {
+        "tokens": T, "us_per_layer": us, "ms_per_step": ms,
+        "kv_bytes_per_layer": kv_bytes, "all_bytes_per_layer": kv_bytes + q_bytes,
+        "gbs_incl_q": (kv_bytes + q_bytes) / (us * 1e-6) / 1e9,
+        "pct_hbm_peak_incl_q": 100.0 * (kv_bytes + q_bytes) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "tokens_per_s": T * LAYERS / (ms * 1e-3),
+    }
+
+
+def cpu_baseline(seconds: float):
+    """The oracle's fp32 decode (oracle/kv_oracle.c orc_decode_cpu_mt) on host
+    cores: one layer of the C4 workload (131072 tokens) per call, repeated for
+    about `seconds`."""
+    import numpy as np
+    import oracle
+    ctx = 131072
+    maxp = ctx // P
+    threads = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    pool = oracle.f32_to_bf16(rng.standard_normal(maxp * P * 512, dtype=np.float32)
+                              / np.float32(128 ** 0.5))
+    pt = rng.permutation(maxp).astype(np.uint32)
+    q = oracle.f32_to_bf16(rng.standard_normal(2560, dtype=np.float32) / np.float32(11.3))
+    oracle.decode_cpu_mt(q, [ctx - 1], [pt], pool, 0, P, maxp, threads)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.decode_cpu_mt(q, [ctx - 1], [pt], pool, 0, P, maxp, threads)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    per_layer = dt / n
+    return {
+        "value": (ctx * KV_BYTES_PER_TOKEN + QO_BYTES) / per_layer / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} single-layer decode steps at 131072 ctx (C4), fp32, "
+                  f"{per_layer * 1e3:.2f} ms/layer",
+        "us_per_layer": per_layer * 1e6,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (the KV path has no "
+              f"multi-GPU code); --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    pkg = importlib.import_module("minicpm5-5080fast_amd")
+    kvm = pkg.kv
+    dev = torch.device("cuda:0")
+    timer = Timer(torch, graphs=not args.eager)
+    cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]
+    res = {}
+    if "c4" in cfgs:
+        log("C4: 128K single session ...")
+        res["c4_128k"] = bench_decode_single(kvm, torch, dev, timer, 131072, args.steps,
+                                             args.warmup, rot=1)
+        log(res["c4_128k"])
+        torch.cuda.empty_cache()
+    if "c3" in cfgs:
+        log("C3: 8 x 2048 batched ...")
+        res["c3_8x2k"] = bench_decode_batch(kvm, torch, dev, timer, 8, 2048, args.steps * 5,
+                                            args.warmup)
+        log(res["c3_8x2k"])
+        torch.cuda.empty_cache()
+    if "c1" in cfgs:
+        log("C1: 2K single session ...")
+        res["c1_2k"] = bench_decode_single(kvm, torch, dev, timer, 2048, args.steps * 5,
+                                           args.warmup, rot=8)
+        log(res["c1_2k"])
+        torch.cuda.empty_cache()
+    if "c2" in cfgs:
+        log("C2: append 8448 tokens ...")
+        res["c2_append_8448"] = bench_append(kvm, torch, dev, timer, 8448, args.steps,
+                                             args.warmup)
+        log(res["c2_append_8448"])
+        torch.cuda.empty_cache()
+
+    head = res.get("c4_128k")
+    cpu = None if args.no_cpu or head is None else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": "decode-attn us/layer & KV HBM GB/s (% peak) at 2K, 8x2K batch, 128K",
+        "value": round(head["kv_gbs"], 2) if head else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4) if head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (bf16 ~N(0,1)/sqrt(128), seeded permuted page tables)",
+        "config": {"workload": "C4: 1 session x 131072 ctx, Hq16/Hkv2/D128, 64-token "
+                               "pages, chunk 256, 2-level merge, phase0 append, 28 layers"},
+        "roofline": None,
+        "cpu_baseline": cpu,
+        "configs": res,
+    }
+    if head:
+        ach = head["chunk_kernel_gbs"]
+        line["roofline"] = {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                            "traffic": None,
+                            "kernel": "decode_chunk_kernel<true,false> (C4 layer)",
+                            "kernel_us": round(head["chunk_kernel_us"], 3)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
