@@ -212,6 +212,17 @@ mc_status_t mc_kv_batch_advance(int32_t* const* d_slot_seq,
                                 uint32_t* const* d_slot_pos, uint32_t n,
                                 void* stream);
 
+/* ---- debug hooks (additive, outside the frozen ABI; the reference keeps
+ * similar mc_debug_* hooks outside it, session.cpp:631-723) ---- */
+
+/* Session state: host seq_len, owned pages, pool layout and the device
+ * addresses of the pool and page table (any pointer may be NULL). */
+mc_status_t mc_debug_session_info(mc_session_t session, uint32_t* seq_len,
+                                  uint32_t* pages_owned, mc_kv_layout_t* layout,
+                                  void** d_pool, void** d_page_table);
+/* Copies the first n token ids of the device sequence (n <= seq_len). */
+mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n);
+
 /* Library build identity, e.g. "minicpm-kv gfx950". */
 const char* mc_kv_build_info(void);
 

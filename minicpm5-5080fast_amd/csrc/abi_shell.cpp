@@ -1,1 +1,873 @@
-// placeholder, replaced below
+// abi_shell.cpp - the stable mc_* ABI (include/minicpm_runtime.h) on HIP:
+// model / session / batch-group lifecycle around the paged KV cache.
+//
+// Semantics follow the reference runtime: option validation and device
+// selection (native/runtime/model.cpp:100-200), one device arena per session
+// sized at create time (session.cpp:58-135,161-318), reset keeps memory and
+// clears ownership (session.cpp:510-544), prefill validation and chunking by
+// 8448 tokens (prefill_executor.cpp:27,55-157), decode validation, the
+// max_new_tokens EOS sentinel and the mock token rule of the weight-free mode
+// (decode_executor.cpp:35-40,70-150,431-553; sampling.cu:50-56), and the batch
+// group's validation / slot rules (batch_group.cpp:223-612,614-859).
+//
+// Weights are outside this build: a model directory holding model.wpk is
+// rejected with MC_E_UNSUPPORTED, any other directory loads in weight-free
+// mode. Unlike the reference's mock (which skips the forward), this mode runs
+// the real KV path every layer on synthetic qkv rows (synth.hip): prefill
+// appends with RoPE and runs the paged prefill attention, decode runs the
+// phase0 decode attention, batch steps run the batched decode attention with
+// per-slot pointer tables. Emitted tokens follow the reference mock rule
+// token = 100 + ((seq_len * 2654435761) ^ rng) % 1000, rng advanced by
+// xorshift32, seeded from the first decode config's seed.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstring>
+#include <string>
+#include <sys/stat.h>
+#include <vector>
+
+#include "error.h"
+#include "kv_common.h"
+#include "kv_internal.h"
+
+namespace mckv {
+namespace {
+
+constexpr uint32_t kLayers = 42;            // generated_model_config.h:13
+constexpr uint32_t kTokensPerPage = 32;     // kv_cache.h:30
+constexpr uint32_t kVocab = 130560;         // generated_model_config.h
+constexpr int32_t kEos = 130073;            // generated_model_config.h:30
+constexpr uint32_t kMaxCtx = 131072;        // generated_model_config.h
+constexpr uint32_t kPrefillChunk = 8448;    // prefill_executor.cpp:27
+constexpr uint32_t kMaxSlots = 8;           // batch_group.cpp:52
+constexpr double kTheta = 5.0e6;            // generated_model_config.h:23
+
+uint32_t xorshift32(uint32_t x) {
+    x ^= x << 13;
+    x ^= x >> 17;
+    x ^= x << 5;
+    return x;
+}
+int32_t mock_token(uint32_t seq_len, uint32_t rng) {
+    const uint32_t h = (seq_len * 2654435761u) ^ rng;
+    return (int32_t)(100u + h % 1000u);
+}
+
+struct DevState {
+    uint32_t seq_len;
+    int32_t next_token;
+};
+
+size_t align256(size_t x) { return (x + 255u) & ~size_t(255); }
+
+struct ModelImpl {
+    int device_id = 0;
+    uint32_t max_sessions = 0;
+    uint32_t max_ctx = 0;
+    std::atomic<uint32_t> live_sessions{0};
+    uint64_t total_vram = 0;
+};
+
+struct SessionImpl {
+    ModelImpl* model = nullptr;
+    hipStream_t stream = nullptr;
+    void* arena = nullptr;
+    size_t arena_bytes = 0;
+    // carved buffers
+    uint16_t* pool = nullptr;
+    uint32_t* d_pt = nullptr;
+    int32_t* d_seq = nullptr;
+    DevState* d_state = nullptr;
+    float* inv_freq = nullptr;
+    uint16_t* qkv = nullptr;       // [chunk][2560]
+    uint16_t* attn_out = nullptr;  // [chunk][2048]
+    float* partials = nullptr;     // decode level-1
+    float* partials2 = nullptr;    // decode level-2
+    float* pf_partials = nullptr;  // prefill split partials
+    mc_kv_allocator_t* kv = nullptr;
+    mc_kv_layout_t layout{};
+    uint32_t chunk_pos = 64, max_chunks = 0, act_rows = 0;
+    // host state
+    uint32_t seq_len = 0;
+    uint32_t rng = 0;
+    bool rng_seeded = false;
+    bool in_group = false;
+    DevState h_state{};
+    int32_t h_tok = 0;
+    mc_runtime_stats_t total{}, since_reset{};
+    uint64_t min_free = ~0ull;
+};
+
+struct GroupImpl {
+    ModelImpl* model = nullptr;
+    hipStream_t stream = nullptr;
+    uint32_t max_slots = 0, max_ctx = 0, chunk_pos = 64, max_chunks = 0;
+    SessionImpl* members[kMaxSlots] = {};
+    void* arena = nullptr;
+    // device tables (fixed addresses) of the current step's members
+    uint32_t** d_pos = nullptr;
+    uint32_t** d_pt = nullptr;
+    uint16_t** d_kv = nullptr;
+    int32_t** d_tok = nullptr;
+    int32_t** d_seq = nullptr;
+    uint16_t* qkv = nullptr;
+    uint16_t* out = nullptr;
+    float* partials = nullptr;
+    float* partials2 = nullptr;
+    float* inv_freq = nullptr;
+    void* h_tables = nullptr;  // pinned staging: 5 x kMaxSlots pointers
+    int32_t* h_tok = nullptr;  // pinned staging of the step's tokens
+    hipEvent_t ev = nullptr;
+    mc_kv_layout_t layout{};
+};
+
+mc_status_t set_device(int id, const char* who) {
+    const hipError_t e = hipSetDevice(id);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("%s: hipSetDevice(%d) failed: %s", who, id, hipGetErrorString(e));
+        return MC_E_CUDA;
+    }
+    return MC_OK;
+}
+
+#define HIP_OR_RETURN(call, what)                          \
+    do {                                                   \
+        const hipError_t _e = (call);                      \
+        if (_e != hipSuccess) return check_hip(_e, what);  \
+    } while (0)
+#define MC_OR_RETURN(call)                 \
+    do {                                   \
+        const mc_status_t _s = (call);     \
+        if (_s != MC_OK) return _s;        \
+    } while (0)
+
+void release_session(SessionImpl* s) {
+    if (s == nullptr) return;
+    (void)hipSetDevice(s->model->device_id);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->kv) mc_kv_allocator_destroy(s->kv);
+    if (s->arena) (void)hipFree(s->arena);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    s->model->live_sessions.fetch_sub(1);
+    delete s;
+}
+
+void release_group(GroupImpl* g) {
+    if (g == nullptr) return;
+    (void)hipSetDevice(g->model->device_id);
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
+    for (uint32_t i = 0; i < kMaxSlots; ++i)
+        if (g->members[i]) {
+            // remove semantics: group work visible to the member's stream
+            if (g->ev) {
+                (void)hipEventRecord(g->ev, g->stream);
+                (void)hipStreamWaitEvent(g->members[i]->stream, g->ev, 0);
+            }
+            g->members[i]->in_group = false;
+            g->members[i] = nullptr;
+        }
+    if (g->ev) (void)hipEventDestroy(g->ev);
+    if (g->h_tables) (void)hipHostFree(g->h_tables);
+    if (g->h_tok) (void)hipHostFree(g->h_tok);
+    if (g->arena) (void)hipFree(g->arena);
+    if (g->stream) (void)hipStreamDestroy(g->stream);
+    delete g;
+}
+
+// Runs the synthetic forward of one prefill chunk: per layer synthetic rows,
+// RoPE + K/V append, paged prefill attention.
+mc_status_t prefill_chunk(SessionImpl& s, uint32_t base, uint32_t n) {
+    hipStream_t st = s.stream;
+    s.h_state.seq_len = base;
+    HIP_OR_RETURN(hipMemcpyAsync(&s.d_state->seq_len, &s.h_state.seq_len, sizeof(uint32_t),
+                                 hipMemcpyHostToDevice, st),
+                  "mc_prefill: d_state H2D failed");
+    const uint32_t S = mc_kv_prefill_split_kv(n);
+    for (uint32_t l = 0; l < kLayers; ++l) {
+        MC_OR_RETURN(launch_synth_qkv(s.qkv, n, s.d_seq + base, &s.d_state->seq_len, l, st));
+        MC_OR_RETURN(mc_kv_rope_append(s.qkv, n, &s.d_state->seq_len, l, s.d_pt, s.pool,
+                                       s.layout, kTheta, s.inv_freq, st));
+        MC_OR_RETURN(mc_kv_attention_prefill(s.qkv, n, &s.d_state->seq_len, l, s.d_pt,
+                                             s.pool, s.layout, s.attn_out,
+                                             S > 1u ? s.pf_partials : nullptr, S, st));
+    }
+    // The stream still reads h_state.seq_len's copy source asynchronously; keep
+    // the host value stable until the caller synchronizes.
+    HIP_OR_RETURN(hipStreamSynchronize(st), "mc_prefill: stream sync failed");
+    return MC_OK;
+}
+
+}  // namespace
+}  // namespace mckv
+
+using namespace mckv;
+
+struct mc_model {
+    ModelImpl* impl;
+};
+struct mc_session {
+    SessionImpl* impl;
+};
+struct mc_batch_group {
+    GroupImpl* impl;
+};
+
+extern "C" {
+
+mc_status_t mc_model_load(const char* model_dir, const mc_model_options_t* options,
+                          mc_model_t* out_model) {
+    MC_GUARD_BEGIN
+    if (out_model) *out_model = mc_model{nullptr};
+    if (model_dir == nullptr || options == nullptr || out_model == nullptr) {
+        set_error("mc_model_load: model_dir/options/out_model is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (options->struct_size != sizeof(mc_model_options_t)) {
+        set_error("mc_model_load: options->struct_size=%u but expected %zu",
+                  options->struct_size, sizeof(mc_model_options_t));
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (options->abi_version != MC_ABI_VERSION) {
+        set_error("mc_model_load: abi_version=0x%08x expected 0x%08x",
+                  options->abi_version, MC_ABI_VERSION);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (options->max_sessions == 0 || options->device_id < 0) {
+        set_error("mc_model_load: max_sessions=%u device_id=%d", options->max_sessions,
+                  options->device_id);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (options->max_context_tokens == 0 || options->max_context_tokens > kMaxCtx) {
+        set_error("mc_model_load: max_context_tokens=%u out of range [1,%u]",
+                  options->max_context_tokens, kMaxCtx);
+        return MC_E_UNSUPPORTED;
+    }
+    if (options->precision != MC_BF16 || options->kv_precision != MC_KV_BF16) {
+        set_error("mc_model_load: only BF16 weights/KV are supported by this build");
+        return MC_E_UNSUPPORTED;
+    }
+    struct stat st {};
+    if (stat(model_dir, &st) != 0 || !S_ISDIR(st.st_mode)) {
+        set_error("mc_model_load: model_dir '%s' is not a readable directory", model_dir);
+        return MC_E_IO;
+    }
+    const std::string wpk = std::string(model_dir) + "/model.wpk";
+    if (stat(wpk.c_str(), &st) == 0) {
+        set_error("mc_model_load: '%s' holds model weights; the weight path (GEMV/GEMM, "
+                  "norms, sampling) is not part of this KV-cache build",
+                  wpk.c_str());
+        return MC_E_UNSUPPORTED;
+    }
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return check_hip(e, "mc_model_load: hipGetDeviceCount failed");
+    if (options->device_id >= count) {
+        set_error("mc_model_load: device_id=%d out of range (device count=%d)",
+                  options->device_id, count);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    MC_OR_RETURN(set_device(options->device_id, "mc_model_load"));
+    hipDeviceProp_t prop{};
+    e = hipGetDeviceProperties(&prop, options->device_id);
+    if (e != hipSuccess) return check_hip(e, "mc_model_load: hipGetDeviceProperties failed");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_error("mc_model_load: device %d is '%s'; this build targets gfx950 (MI355X)",
+                  options->device_id, prop.gcnArchName);
+        return MC_E_MODEL_MISMATCH;
+    }
+    auto* m = new ModelImpl();
+    m->device_id = options->device_id;
+    m->max_sessions = options->max_sessions;
+    m->max_ctx = options->max_context_tokens;
+    m->total_vram = prop.totalGlobalMem;
+    *out_model = mc_model{m};
+    return MC_OK;
+    MC_GUARD_END
+}
+
+void mc_model_destroy(mc_model_t model) { delete model.impl; }
+
+mc_status_t mc_session_create(mc_model_t model, mc_session_t* out_session) {
+    MC_GUARD_BEGIN
+    if (out_session) *out_session = mc_session{nullptr};
+    if (model.impl == nullptr || out_session == nullptr) {
+        set_error("mc_session_create: model/out_session is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    ModelImpl* m = model.impl;
+    MC_OR_RETURN(set_device(m->device_id, "mc_session_create"));
+    if (m->live_sessions.fetch_add(1) + 1 > m->max_sessions) {
+        m->live_sessions.fetch_sub(1);
+        set_error("mc_session_create: session limit reached (max_sessions=%u)",
+                  m->max_sessions);
+        return MC_E_UNSUPPORTED;
+    }
+    auto* s = new SessionImpl();
+    s->model = m;
+    hipError_t e = hipStreamCreate(&s->stream);
+    if (e != hipSuccess) {
+        release_session(s);
+        return check_hip(e, "mc_session_create: hipStreamCreate failed");
+    }
+    const uint32_t max_pages = (m->max_ctx + kTokensPerPage - 1u) / kTokensPerPage;
+    s->layout = mc_kv_layout_t{max_pages, kTokensPerPage, kLayers, 0};
+    s->chunk_pos = mc_kv_decode_chunk_pos(m->max_ctx);
+    s->max_chunks = mc_kv_decode_max_chunks(m->max_ctx, s->chunk_pos);
+    s->act_rows = m->max_ctx < kPrefillChunk ? m->max_ctx : kPrefillChunk;
+    const size_t pool_b = (size_t)mc_kv_total_elems(s->layout) * 2u;
+    const size_t sizes[] = {
+        pool_b,
+        (size_t)max_pages * 4u,
+        (size_t)m->max_ctx * 4u,
+        sizeof(DevState),
+        64u * 4u,
+        (size_t)s->act_rows * kRow * 2u,
+        (size_t)s->act_rows * 2048u * 2u,
+        (size_t)kHq * s->max_chunks * kPartial * 4u,
+        (size_t)kHq * kSplit2 * kPartial * 4u,
+        (size_t)4096u * kHq * kPartial * 4u,  // prefill: T * S_kv <= 4096
+    };
+    size_t total = 0;
+    for (size_t b : sizes) total += align256(b);
+    e = hipMalloc(&s->arena, total);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        size_t fr = 0, tt = 0;
+        (void)hipMemGetInfo(&fr, &tt);
+        set_error("mc_session_create: session arena allocation failed: need %zu bytes but "
+                  "free VRAM is %zu bytes (max_context_tokens=%u)",
+                  total, fr, m->max_ctx);
+        release_session(s);
+        return MC_E_OUT_OF_MEMORY;
+    }
+    s->arena_bytes = total;
+    char* p = static_cast<char*>(s->arena);
+    void* bufs[10];
+    for (int i = 0; i < 10; ++i) {
+        bufs[i] = p;
+        p += align256(sizes[i]);
+    }
+    s->pool = (uint16_t*)bufs[0];
+    s->d_pt = (uint32_t*)bufs[1];
+    s->d_seq = (int32_t*)bufs[2];
+    s->d_state = (DevState*)bufs[3];
+    s->inv_freq = (float*)bufs[4];
+    s->qkv = (uint16_t*)bufs[5];
+    s->attn_out = (uint16_t*)bufs[6];
+    s->partials = (float*)bufs[7];
+    s->partials2 = (float*)bufs[8];
+    s->pf_partials = (float*)bufs[9];
+    mc_status_t rs = mc_kv_allocator_create(s->d_pt, max_pages, kTokensPerPage, &s->kv);
+    if (rs == MC_OK) rs = mc_kv_rope_inv_freq_init(s->inv_freq, kTheta, s->stream);
+    if (rs == MC_OK) {
+        e = hipMemsetAsync(s->d_state, 0, sizeof(DevState), s->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) rs = check_hip(e, "mc_session_create: init failed");
+    }
+    if (rs != MC_OK) {
+        release_session(s);
+        return rs;
+    }
+    *out_session = mc_session{s};
+    return MC_OK;
+    MC_GUARD_END
+}
+
+mc_status_t mc_session_reset(mc_session_t session) {
+    MC_GUARD_BEGIN
+    SessionImpl* s = session.impl;
+    if (s == nullptr) {
+        set_error("mc_session_reset: session is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    MC_OR_RETURN(set_device(s->model->device_id, "mc_session_reset"));
+    mc_kv_allocator_release_all(s->kv);
+    s->seq_len = 0;
+    s->rng_seeded = false;
+    s->since_reset = mc_runtime_stats_t{};
+    s->h_state = DevState{};
+    HIP_OR_RETURN(hipMemcpyAsync(s->d_state, &s->h_state, sizeof(DevState),
+                                 hipMemcpyHostToDevice, s->stream),
+                  "mc_session_reset: d_state H2D failed");
+    HIP_OR_RETURN(hipStreamSynchronize(s->stream), "mc_session_reset: sync failed");
+    return MC_OK;
+    MC_GUARD_END
+}
+
+void mc_session_destroy(mc_session_t session) { release_session(session.impl); }
+
+mc_status_t mc_prefill(mc_session_t session, const int32_t* token_ids,
+                       uint32_t token_count) {
+    MC_GUARD_BEGIN
+    SessionImpl* s = session.impl;
+    if (s == nullptr) {
+        set_error("mc_prefill: session is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (token_ids == nullptr || token_count == 0) {
+        set_error("mc_prefill: token_ids is NULL or token_count is 0");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (s->in_group) {
+        set_error("mc_prefill: session is a member of a batch group");
+        return MC_E_UNSUPPORTED;
+    }
+    const uint32_t max_ctx = s->model->max_ctx;
+    if (token_count > max_ctx - s->seq_len) {
+        set_error("mc_prefill: token_count=%u would exceed max_context_tokens=%u "
+                  "(seq_len=%u)",
+                  token_count, max_ctx, s->seq_len);
+        return MC_E_OUT_OF_MEMORY;
+    }
+    for (uint32_t i = 0; i < token_count; ++i)
+        if (token_ids[i] < 0 || (uint32_t)token_ids[i] >= kVocab) {
+            set_error("mc_prefill: token_ids[%u]=%d out of range [0,%u)", i, token_ids[i],
+                      kVocab);
+            return MC_E_INVALID_ARGUMENT;
+        }
+    MC_OR_RETURN(set_device(s->model->device_id, "mc_prefill"));
+    const auto t0 = std::chrono::steady_clock::now();
+    const uint32_t base = s->seq_len;
+    HIP_OR_RETURN(hipMemcpyAsync(s->d_seq + base, token_ids, (size_t)token_count * 4u,
+                                 hipMemcpyHostToDevice, s->stream),
+                  "mc_prefill: token H2D copy failed");
+    MC_OR_RETURN(mc_kv_allocator_ensure_pages_for(s->kv, base + token_count, s->stream));
+    for (uint32_t off = 0; off < token_count;) {
+        const uint32_t n =
+            token_count - off > s->act_rows ? s->act_rows : token_count - off;
+        MC_OR_RETURN(prefill_chunk(*s, base + off, n));
+        off += n;
+    }
+    s->seq_len = base + token_count;
+    s->h_state.seq_len = s->seq_len;
+    s->h_state.next_token = token_ids[token_count - 1];
+    HIP_OR_RETURN(hipMemcpyAsync(s->d_state, &s->h_state, sizeof(DevState),
+                                 hipMemcpyHostToDevice, s->stream),
+                  "mc_prefill: d_state H2D update failed");
+    HIP_OR_RETURN(hipStreamSynchronize(s->stream), "mc_prefill: stream sync failed");
+    const uint64_t us = (uint64_t)std::chrono::duration_cast<std::chrono::microseconds>(
+                            std::chrono::steady_clock::now() - t0)
+                            .count();
+    s->total.prompt_tokens += token_count;
+    s->since_reset.prompt_tokens += token_count;
+    s->total.prefill_us += us;
+    s->since_reset.prefill_us += us;
+    return MC_OK;
+    MC_GUARD_END
+}
+
+mc_status_t mc_decode_one(mc_session_t session, const mc_generation_config_t* config,
+                          int32_t* out_token) {
+    MC_GUARD_BEGIN
+    SessionImpl* s = session.impl;
+    if (s == nullptr || config == nullptr || out_token == nullptr) {
+        set_error("mc_decode_one: session/config/out_token is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (config->struct_size != sizeof(*config)) {
+        set_error("mc_decode_one: config->struct_size=%u but expected %zu",
+                  config->struct_size, sizeof(*config));
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (config->max_new_tokens == 0) {
+        set_error("mc_decode_one: max_new_tokens must be > 0");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (s->in_group) {
+        set_error("mc_decode_one: session is a member of a batch group");
+        return MC_E_UNSUPPORTED;
+    }
+    if (s->seq_len == 0) {
+        set_error("mc_decode_one: sequence is empty (call mc_prefill first)");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (s->seq_len >= s->model->max_ctx) {
+        set_error("mc_decode_one: context is full (seq_len=%u, max=%u)", s->seq_len,
+                  s->model->max_ctx);
+        return MC_E_OUT_OF_MEMORY;
+    }
+    if (s->since_reset.generated_tokens >= config->max_new_tokens) {
+        *out_token = kEos;
+        return MC_OK;
+    }
+    if (!s->rng_seeded) {
+        s->rng = (uint32_t)config->seed;
+        s->rng_seeded = true;
+    }
+    MC_OR_RETURN(set_device(s->model->device_id, "mc_decode_one"));
+    const auto t0 = std::chrono::steady_clock::now();
+    hipStream_t st = s->stream;
+    MC_OR_RETURN(mc_kv_allocator_ensure_pages_for(s->kv, s->seq_len + 1u, st));
+    // Per layer: synthetic row of (d_next_token, seq_len), phase0 decode
+    // attention at limit = seq_len (appends K/V of that position).
+    for (uint32_t l = 0; l < kLayers; ++l) {
+        MC_OR_RETURN(launch_synth_qkv(s->qkv, 1, &s->d_state->next_token,
+                                      &s->d_state->seq_len, l, st));
+        MC_OR_RETURN(mc_kv_attention_decode(s->qkv, &s->d_state->seq_len, l, s->d_pt,
+                                            s->pool, s->layout, s->partials, s->max_chunks,
+                                            s->attn_out, st, s->inv_freq, s->chunk_pos,
+                                            s->partials2));
+    }
+    s->h_tok = mock_token(s->seq_len, s->rng);
+    HIP_OR_RETURN(hipMemcpyAsync(&s->d_state->next_token, &s->h_tok, 4u,
+                                 hipMemcpyHostToDevice, st),
+                  "mc_decode_one: token H2D failed");
+    MC_OR_RETURN(mc_kv_decode_advance(s->d_seq, &s->d_state->next_token,
+                                      &s->d_state->seq_len, st));
+    HIP_OR_RETURN(hipStreamSynchronize(st), "mc_decode_one: stream sync failed");
+    s->seq_len += 1;
+    s->h_state.seq_len = s->seq_len;
+    s->h_state.next_token = s->h_tok;
+    s->rng = xorshift32(s->rng);
+    const uint64_t us = (uint64_t)std::chrono::duration_cast<std::chrono::microseconds>(
+                            std::chrono::steady_clock::now() - t0)
+                            .count();
+    s->total.generated_tokens += 1;
+    s->since_reset.generated_tokens += 1;
+    s->total.decode_us += us;
+    s->since_reset.decode_us += us;
+    *out_token = s->h_tok;
+    return MC_OK;
+    MC_GUARD_END
+}
+
+mc_status_t mc_get_stats(mc_session_t session, mc_runtime_stats_t* out_stats) {
+    MC_GUARD_BEGIN
+    SessionImpl* s = session.impl;
+    if (s == nullptr || out_stats == nullptr) {
+        set_error("mc_get_stats: session/out_stats is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    MC_OR_RETURN(set_device(s->model->device_id, "mc_get_stats"));
+    size_t fr = 0, tt = 0;
+    HIP_OR_RETURN(hipMemGetInfo(&fr, &tt), "mc_get_stats: hipMemGetInfo failed");
+    if (fr < s->min_free) s->min_free = fr;
+    *out_stats = s->total;
+    out_stats->peak_vram_bytes = s->model->total_vram - s->min_free;
+    out_stats->cuda_graph_launches = 0;
+    return MC_OK;
+    MC_GUARD_END
+}
+
+// ---------------- batch group ----------------
+
+mc_status_t mc_batch_group_create(mc_model_t model, const mc_batch_options_t* options,
+                                  mc_batch_group_t* out_group) {
+    MC_GUARD_BEGIN
+    if (out_group) *out_group = mc_batch_group{nullptr};
+    if (model.impl == nullptr) {
+        set_error("mc_batch_group_create: model is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (options == nullptr || out_group == nullptr) {
+        set_error("mc_batch_group_create: options/out_group is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (options->struct_size != sizeof(mc_batch_options_t)) {
+        set_error("mc_batch_group_create: options->struct_size=%u but expected %zu",
+                  options->struct_size, sizeof(mc_batch_options_t));
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (options->abi_version != MC_ABI_VERSION) {
+        set_error("mc_batch_group_create: abi_version=0x%08x expected 0x%08x",
+                  options->abi_version, MC_ABI_VERSION);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    for (uint32_t i = 0; i < 4; ++i)
+        if (options->reserved[i] != 0) {
+            set_error("mc_batch_group_create: reserved[%u] must be zero", i);
+            return MC_E_INVALID_ARGUMENT;
+        }
+    if (options->max_slots == 0 || options->max_slots > kMaxSlots) {
+        set_error("mc_batch_group_create: max_slots=%u out of range [1,%u]",
+                  options->max_slots, kMaxSlots);
+        return MC_E_UNSUPPORTED;
+    }
+    ModelImpl* m = model.impl;
+    if (options->max_context_tokens != m->max_ctx) {
+        set_error("mc_batch_group_create: max_context_tokens=%u must equal the model's %u",
+                  options->max_context_tokens, m->max_ctx);
+        return MC_E_UNSUPPORTED;
+    }
+    MC_OR_RETURN(set_device(m->device_id, "mc_batch_group_create"));
+    auto* g = new GroupImpl();
+    g->model = m;
+    g->max_slots = options->max_slots;
+    g->max_ctx = m->max_ctx;
+    g->chunk_pos = mc_kv_decode_chunk_pos(m->max_ctx);
+    g->max_chunks = mc_kv_decode_max_chunks(m->max_ctx, g->chunk_pos);
+    hipError_t e = hipStreamCreate(&g->stream);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&g->ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        release_group(g);
+        return check_hip(e, "mc_batch_group_create: stream/event creation failed");
+    }
+    const uint32_t B = kMaxSlots;
+    const size_t sizes[] = {
+        5u * B * sizeof(void*),
+        (size_t)B * kRow * 2u,
+        (size_t)B * 2048u * 2u,
+        (size_t)B * kHq * g->max_chunks * kPartial * 4u,
+        (size_t)B * kHq * kSplit2 * kPartial * 4u,
+        64u * 4u,
+    };
+    size_t total = 0;
+    for (size_t b : sizes) total += align256(b);
+    e = hipMalloc(&g->arena, total);
+    if (e == hipSuccess) e = hipHostMalloc(&g->h_tables, 5u * B * sizeof(void*));
+    if (e == hipSuccess) e = hipHostMalloc((void**)&g->h_tok, B * sizeof(int32_t));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("mc_batch_group_create: allocation failed (need %zu bytes)", total);
+        release_group(g);
+        return MC_E_OUT_OF_MEMORY;
+    }
+    char* p = static_cast<char*>(g->arena);
+    void** tables = reinterpret_cast<void**>(p);
+    g->d_pos = reinterpret_cast<uint32_t**>(tables);
+    g->d_pt = reinterpret_cast<uint32_t**>(tables + B);
+    g->d_kv = reinterpret_cast<uint16_t**>(tables + 2u * B);
+    g->d_tok = reinterpret_cast<int32_t**>(tables + 3u * B);
+    g->d_seq = reinterpret_cast<int32_t**>(tables + 4u * B);
+    p += align256(sizes[0]);
+    g->qkv = (uint16_t*)p;
+    p += align256(sizes[1]);
+    g->out = (uint16_t*)p;
+    p += align256(sizes[2]);
+    g->partials = (float*)p;
+    p += align256(sizes[3]);
+    g->partials2 = (float*)p;
+    p += align256(sizes[4]);
+    g->inv_freq = (float*)p;
+    mc_status_t rs = mc_kv_rope_inv_freq_init(g->inv_freq, kTheta, g->stream);
+    if (rs == MC_OK) {
+        e = hipStreamSynchronize(g->stream);
+        if (e != hipSuccess) rs = check_hip(e, "mc_batch_group_create: init sync failed");
+    }
+    if (rs != MC_OK) {
+        release_group(g);
+        return rs;
+    }
+    *out_group = mc_batch_group{g};
+    return MC_OK;
+    MC_GUARD_END
+}
+
+mc_status_t mc_batch_group_add(mc_batch_group_t group, mc_session_t session,
+                               uint32_t* slot_id) {
+    MC_GUARD_BEGIN
+    GroupImpl* g = group.impl;
+    if (g == nullptr) {
+        set_error("mc_batch_group_add: group is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    SessionImpl* s = session.impl;
+    if (s == nullptr || slot_id == nullptr) {
+        set_error("mc_batch_group_add: session/slot_id is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (s->model != g->model) {
+        set_error("mc_batch_group_add: session belongs to a different model");
+        return MC_E_UNSUPPORTED;
+    }
+    if (s->chunk_pos != g->chunk_pos || s->max_chunks != g->max_chunks) {
+        set_error("mc_batch_group_add: ctx/chunk tier mismatch");
+        return MC_E_UNSUPPORTED;
+    }
+    if (s->in_group) {
+        set_error("mc_batch_group_add: session is already in a batch group");
+        return MC_E_UNSUPPORTED;
+    }
+    uint32_t slot = g->max_slots;
+    for (uint32_t i = 0; i < g->max_slots; ++i)
+        if (g->members[i] == nullptr) {
+            slot = i;
+            break;
+        }
+    if (slot == g->max_slots) {
+        set_error("mc_batch_group_add: group is full (max_slots=%u)", g->max_slots);
+        return MC_E_UNSUPPORTED;
+    }
+    MC_OR_RETURN(set_device(g->model->device_id, "mc_batch_group_add"));
+    // member -> group: the member's earlier prefill/KV writes are visible.
+    HIP_OR_RETURN(hipEventRecord(g->ev, s->stream),
+                  "mc_batch_group_add: event chain (member->group) failed");
+    HIP_OR_RETURN(hipStreamWaitEvent(g->stream, g->ev, 0),
+                  "mc_batch_group_add: event chain (member->group) failed");
+    g->members[slot] = s;
+    s->in_group = true;
+    *slot_id = slot;
+    return MC_OK;
+    MC_GUARD_END
+}
+
+mc_status_t mc_batch_group_remove(mc_batch_group_t group, uint32_t slot_id) {
+    MC_GUARD_BEGIN
+    GroupImpl* g = group.impl;
+    if (g == nullptr) {
+        set_error("mc_batch_group_remove: group is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (slot_id >= g->max_slots || g->members[slot_id] == nullptr) {
+        set_error("mc_batch_group_remove: slot %u has no member", slot_id);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    SessionImpl* s = g->members[slot_id];
+    MC_OR_RETURN(set_device(g->model->device_id, "mc_batch_group_remove"));
+    // group -> member: the group's KV / sequence writes are visible to solo use.
+    HIP_OR_RETURN(hipEventRecord(g->ev, g->stream),
+                  "mc_batch_group_remove: event chain (group->member) failed");
+    HIP_OR_RETURN(hipStreamWaitEvent(s->stream, g->ev, 0),
+                  "mc_batch_group_remove: event chain (group->member) failed");
+    s->in_group = false;
+    g->members[slot_id] = nullptr;
+    return MC_OK;
+    MC_GUARD_END
+}
+
+mc_status_t mc_batch_step(mc_batch_group_t group, const uint32_t* slot_ids, uint32_t n,
+                          const mc_generation_config_t* cfgs, int32_t* out_tokens) {
+    MC_GUARD_BEGIN
+    GroupImpl* g = group.impl;
+    if (g == nullptr) {
+        set_error("mc_batch_step: group is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (slot_ids == nullptr || cfgs == nullptr || out_tokens == nullptr) {
+        set_error("mc_batch_step: slot_ids/cfgs/out_tokens is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (n == 0 || n > g->max_slots) {
+        set_error("mc_batch_step: n=%u out of range [1,%u]", n, g->max_slots);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t sid = slot_ids[i];
+        if (sid >= g->max_slots || g->members[sid] == nullptr) {
+            set_error("mc_batch_step: slot_ids[%u]=%u has no member", i, sid);
+            return MC_E_INVALID_ARGUMENT;
+        }
+        for (uint32_t j = 0; j < i; ++j)
+            if (slot_ids[j] == sid) {
+                set_error("mc_batch_step: duplicate slot %u", sid);
+                return MC_E_INVALID_ARGUMENT;
+            }
+        if (cfgs[i].struct_size != sizeof(cfgs[i])) {
+            set_error("mc_batch_step: cfgs[%u].struct_size=%u but expected %zu", i,
+                      cfgs[i].struct_size, sizeof(cfgs[i]));
+            return MC_E_INVALID_ARGUMENT;
+        }
+        if (cfgs[i].temperature > 0.f && cfgs[i].top_k != 1u) {
+            set_error("mc_batch_step: non-greedy cfgs[%u] unsupported (greedy only)", i);
+            return MC_E_UNSUPPORTED;
+        }
+    }
+    MC_OR_RETURN(set_device(g->model->device_id, "mc_batch_step"));
+    hipStream_t st = g->stream;
+    for (uint32_t i = 0; i < n; ++i) {
+        SessionImpl* s = g->members[slot_ids[i]];
+        if (s->seq_len == 0) {
+            set_error("mc_batch_step: slot %u sequence is empty (prefill first)",
+                      slot_ids[i]);
+            return MC_E_INVALID_ARGUMENT;
+        }
+        if (s->seq_len >= g->max_ctx) {
+            set_error("mc_batch_step: slot %u context is full (seq_len=%u)", slot_ids[i],
+                      s->seq_len);
+            return MC_E_OUT_OF_MEMORY;
+        }
+    }
+    for (uint32_t i = 0; i < n; ++i)
+        MC_OR_RETURN(mc_kv_allocator_ensure_pages_for(g->members[slot_ids[i]]->kv,
+                                                      g->members[slot_ids[i]]->seq_len + 1u,
+                                                      st));
+    const auto t0 = std::chrono::steady_clock::now();
+    // Step tables (compacted to the n members of this step).
+    void** h = static_cast<void**>(g->h_tables);
+    const uint32_t B = kMaxSlots;
+    for (uint32_t i = 0; i < n; ++i) {
+        SessionImpl* s = g->members[slot_ids[i]];
+        h[i] = &s->d_state->seq_len;
+        h[B + i] = s->d_pt;
+        h[2u * B + i] = s->pool;
+        h[3u * B + i] = &s->d_state->next_token;
+        h[4u * B + i] = s->d_seq;
+    }
+    HIP_OR_RETURN(hipMemcpyAsync(g->d_pos, h, 5u * B * sizeof(void*),
+                                 hipMemcpyHostToDevice, st),
+                  "mc_batch_step: slot pointer table H2D failed");
+    const mc_kv_layout_t lay = g->members[slot_ids[0]]->layout;
+    for (uint32_t l = 0; l < kLayers; ++l) {
+        MC_OR_RETURN(launch_synth_qkv_batch(g->qkv, n, g->d_tok, g->d_pos, l, st));
+        MC_OR_RETURN(mc_kv_attention_decode_batch(
+            g->qkv, g->d_pos, n, l, g->d_pt, g->d_kv, lay, g->partials, g->max_chunks,
+            g->out, st, g->inv_freq, g->chunk_pos, g->partials2));
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        SessionImpl* s = g->members[slot_ids[i]];
+        if (!s->rng_seeded) {
+            s->rng = (uint32_t)cfgs[i].seed;
+            s->rng_seeded = true;
+        }
+        g->h_tok[i] = mock_token(s->seq_len, s->rng);
+        HIP_OR_RETURN(hipMemcpyAsync(&s->d_state->next_token, &g->h_tok[i], 4u,
+                                     hipMemcpyHostToDevice, st),
+                      "mc_batch_step: token H2D failed");
+    }
+    MC_OR_RETURN(mc_kv_batch_advance(g->d_seq, g->d_tok, g->d_pos, n, st));
+    HIP_OR_RETURN(hipStreamSynchronize(st), "mc_batch_step: stream sync failed");
+    const uint64_t us = (uint64_t)std::chrono::duration_cast<std::chrono::microseconds>(
+                            std::chrono::steady_clock::now() - t0)
+                            .count();
+    for (uint32_t i = 0; i < n; ++i) {
+        SessionImpl* s = g->members[slot_ids[i]];
+        s->seq_len += 1;
+        s->h_state.seq_len = s->seq_len;
+        s->h_state.next_token = g->h_tok[i];
+        s->rng = xorshift32(s->rng);
+        s->total.generated_tokens += 1;
+        s->since_reset.generated_tokens += 1;
+        s->total.decode_us += us;
+        s->since_reset.decode_us += us;
+        out_tokens[i] = g->h_tok[i];
+    }
+    return MC_OK;
+    MC_GUARD_END
+}
+
+void mc_batch_group_destroy(mc_batch_group_t group) { release_group(group.impl); }
+
+// ---------------- debug hooks (outside the frozen ABI) ----------------
+
+mc_status_t mc_debug_session_info(mc_session_t session, uint32_t* seq_len,
+                                  uint32_t* pages_owned, mc_kv_layout_t* layout,
+                                  void** d_pool, void** d_page_table) {
+    SessionImpl* s = session.impl;
+    if (s == nullptr) {
+        set_error("mc_debug_session_info: session is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (seq_len) *seq_len = s->seq_len;
+    if (pages_owned) *pages_owned = mc_kv_allocator_pages_owned(s->kv);
+    if (layout) *layout = s->layout;
+    if (d_pool) *d_pool = s->pool;
+    if (d_page_table) *d_page_table = s->d_pt;
+    return MC_OK;
+}
+
+mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n) {
+    SessionImpl* s = session.impl;
+    if (s == nullptr || out == nullptr || n > s->seq_len) {
+        set_error("mc_debug_session_seq: bad arguments");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    MC_OR_RETURN(set_device(s->model->device_id, "mc_debug_session_seq"));
+    HIP_OR_RETURN(hipMemcpy(out, s->d_seq, (size_t)n * 4u, hipMemcpyDeviceToHost),
+                  "mc_debug_session_seq: D2H failed");
+    return MC_OK;
+}
+
+}  // extern "C"

@@ -63,6 +63,28 @@ constexpr uint32_t kThreads = 256;
 constexpr uint32_t kWaves = 4;
 constexpr uint32_t kTile = 16;
 
+// Tuning knobs (compile-time): tiles in flight per wave beyond the one being
+// computed, forced waves per SIMD (0 = compiler choice), streaming loads.
+#ifndef MCKV_PREFETCH
+#define MCKV_PREFETCH 1
+#endif
+#ifndef MCKV_WAVES_PER_EU
+#define MCKV_WAVES_PER_EU 0
+#endif
+#ifndef MCKV_NT_LOADS
+#define MCKV_NT_LOADS 0
+#endif
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) {
+#if MCKV_NT_LOADS
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(uint4, __builtin_nontemporal_load(
+                                         reinterpret_cast<const u32x4*>(p)));
+#else
+    return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
 struct Tile {
     uint4 k[4];
     uint4 v[4];
@@ -92,21 +114,28 @@ struct DecodeArgs {
     uint16_t* out;    // this slot: [2048]
 };
 
+// One workgroup processes chunks [c_first, c_first + cpw) of one (slot, kv
+// head). Waves take tiles j = wave, wave+4, ... of each chunk; the next tile's
+// loads are issued before the current tile computes, also across a chunk
+// boundary, so the memory pipeline never drains between chunks. At the end of
+// every chunk the 4 wave states are folded through LDS (double-buffered by
+// chunk parity, one barrier per chunk) and the partial (or, for a single-chunk
+// context, the output) is written. cpw > 1 requires C % 64 == 0.
 template <bool PH0>
-__device__ __forceinline__ void decode_chunk_body(const DecodeArgs a, uint32_t layer,
+__device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t layer,
                                                   DevLayout ly, uint32_t NC,
                                                   const float* __restrict__ inv_freq,
                                                   uint32_t C, uint32_t kvh,
-                                                  uint32_t chunk) {
+                                                  uint32_t c_first, uint32_t cpw) {
     __shared__ float s_cs[64], s_sn[64];
-    __shared__ float s_m[kWaves][kGroup], s_l[kWaves][kGroup];
-    __shared__ __align__(16) float s_acc[kWaves][kGroup][kD];
+    __shared__ __align__(16) uint16_t s_fresh[256];  // phase0: K | V of `limit`
+    __shared__ float s_m[2][kWaves][kGroup], s_l[2][kWaves][kGroup];
+    __shared__ __align__(16) float s_acc[2][kWaves][kGroup][kD];
 
     const uint32_t limit = a.limit;
-    const uint32_t start = chunk * C;
-    if (start > limit) return;  // uniform over the block
-    const uint32_t end = min(start + C - 1u, limit);
-    const uint32_t ntiles = (end - start) / kTile + 1u;
+    const uint32_t nvalid = min(limit / C + 1u, NC);
+    if (c_first >= nvalid) return;  // uniform over the block
+    const uint32_t c_end = min(c_first + cpw, nvalid);
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63u;
@@ -118,76 +147,68 @@ __device__ __forceinline__ void decode_chunk_body(const DecodeArgs a, uint32_t l
     uint16_t* __restrict__ pool = a.pool;
     const uint32_t kvcol = kvh * kD + 8u * grp;  // within a token's K or V half
 
-    // Fresh K/V of position `limit` (phase0): this lane's 4x8 dims.
-    auto fresh_kv = [&](Tile& T) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            T.k[m] = *reinterpret_cast<const uint4*>(q_row + kKCol + kvcol + 32u * m);
-            T.v[m] = *reinterpret_cast<const uint4*>(q_row + kVCol + kvcol + 32u * m);
-        }
-    };
-    auto load_tile = [&](Tile& T, uint32_t t) {
-        const uint32_t p = min(start + t * kTile + tok, end);
-        if (PH0 && p == limit) {
-            fresh_kv(T);  // rotated below, after the cos/sin table exists
-            return;
-        }
+    auto chunk_end = [&](uint32_t c) { return min(c * C + C - 1u, limit); };
+    auto chunk_tiles = [&](uint32_t c) { return (chunk_end(c) - c * C) / kTile + 1u; };
+    auto load_tile = [&](Tile& T, uint32_t c, uint32_t j) {
+        const uint32_t p = min(c * C + j * kTile + tok, chunk_end(c));
         const uint32_t page = pt[p >> ly.log2p];
         const uint16_t* src = pool + token_base(ly, layer, page, p & ly.pmask) + kvcol;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            T.k[m] = *reinterpret_cast<const uint4*>(src + 32u * m);
-            T.v[m] = *reinterpret_cast<const uint4*>(src + 256u + 32u * m);
+            T.k[m] = ld16(src + 32u * m);
+            T.v[m] = ld16(src + 256u + 32u * m);
         }
+    };
+    // Next (chunk, tile) of this wave after (c, j); returns false at the end.
+    auto advance = [&](uint32_t& c, uint32_t& j) {
+        j += kWaves;
+        while (c < c_end && j >= chunk_tiles(c)) {
+            ++c;
+            j = wave;
+        }
+        return c < c_end;
     };
 
     Tile cur;
-    uint32_t t = wave;
-    if (t < ntiles) load_tile(cur, t);
+    uint32_t lc = c_first, lj = wave;  // the tile held in `cur` once loaded
+    bool have = wave < chunk_tiles(c_first) || advance(lc, lj);
+    if (have) load_tile(cur, lc, lj);
 
+    // Phase0 set-up: cos/sin of position `limit`; the block owning `limit`
+    // builds the rotated K and the V of that token in LDS and stores both to
+    // the pool. Lanes whose tile row is `limit` take these values from LDS
+    // (their pool load of that slot may race with the store and is replaced).
+    const bool owner = PH0 && limit / C < c_end && limit < NC * C;
     if (PH0) {
         if (tid < 64u) {
-            float c, s;
-            rope_sincos((float)limit * inv_freq[tid], &c, &s);
+            float c, sn;
+            rope_sincos((float)limit * inv_freq[tid], &c, &sn);
             s_cs[tid] = c;
-            s_sn[tid] = s;
+            s_sn[tid] = sn;
+        }
+        __syncthreads();
+        if (owner && tid < 64u) {
+            const uint16_t* kr = q_row + kKCol + kvh * kD;
+            const uint16_t* vr = q_row + kVCol + kvh * kD;
+            const float x = bf16_to_f32(kr[tid]), x2 = bf16_to_f32(kr[tid + 64u]);
+            const uint16_t lo = f32_to_bf16(rope_rotate(x, x2, s_cs[tid], s_sn[tid], true));
+            const uint16_t hi =
+                f32_to_bf16(rope_rotate(x2, x, s_cs[tid], s_sn[tid], false));
+            const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vr + 2u * tid);
+            s_fresh[tid] = lo;
+            s_fresh[tid + 64u] = hi;
+            *reinterpret_cast<uint32_t*>(&s_fresh[128u + 2u * tid]) = v2;
+            const uint32_t page = pt[limit >> ly.log2p];
+            uint16_t* dst = pool + token_base(ly, layer, page, limit & ly.pmask) + kvh * kD;
+            dst[tid] = lo;
+            dst[tid + 64u] = hi;
+            *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = v2;
         }
         __syncthreads();
     }
 
-    // Rotates the k half of a fresh tile in place and stores K/V of `limit`.
-    auto finish_fresh = [&](Tile& T, uint32_t tt) {
-        if (!PH0) return;
-        const uint32_t p = min(start + tt * kTile + tok, end);
-        if (p != limit) return;
-        uint4 rk[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const uint16_t* x = reinterpret_cast<const uint16_t*>(&T.k[m]);
-            const uint16_t* x2 = reinterpret_cast<const uint16_t*>(&T.k[m ^ 2]);
-            uint16_t* o = reinterpret_cast<uint16_t*>(&rk[m]);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t pr = 32u * (m & 1) + 8u * grp + i;
-                o[i] = f32_to_bf16(rope_rotate(bf16_to_f32(x[i]), bf16_to_f32(x2[i]),
-                                               s_cs[pr], s_sn[pr], m < 2));
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) T.k[m] = rk[m];
-        if (start + tt * kTile + tok == limit) {  // the real row writes the pool
-            const uint32_t page = pt[limit >> ly.log2p];
-            uint16_t* dst =
-                pool + token_base(ly, layer, page, limit & ly.pmask) + kvcol;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                *reinterpret_cast<uint4*>(dst + 32u * m) = T.k[m];
-                *reinterpret_cast<uint4*>(dst + 256u + 32u * m) = T.v[m];
-            }
-        }
-    };
-
     // Q^T B operand: lane holds q[head = tok][32m + 8*grp + i]; heads >= 8 zero.
+    // Phase0 rotates q in registers (partner dim d^64 sits in block m^2).
     bf16x8 qb[4];
     {
         uint4 qr[4];
@@ -225,126 +246,149 @@ __device__ __forceinline__ void decode_chunk_body(const DecodeArgs a, uint32_t l
     for (int i = 0; i < 4; ++i)
         ident[i] = (4u * grp + (uint32_t)i == tok) ? (short)0x3F80 : (short)0;
 
-    float m_run = -INFINITY, l_run = 0.f;
-    f32x4 acc[4][2];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) acc[m][h] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    for (; t < ntiles; t += kWaves) {
-        const bool has_next = t + kWaves < ntiles;
-        Tile nxt;
-        if (has_next) load_tile(nxt, t + kWaves);
-        finish_fresh(cur, t);
-
-        // S^T = K x Q^T
-        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c = c_first; c < c_end; ++c) {
+        const uint32_t cstart = c * C;
+        const uint32_t cend = chunk_end(c);
+        float m_run = -INFINITY, l_run = 0.f;
+        f32x4 acc[4][2];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.k[m]), qb[m], s,
-                                                        0, 0, 0);
-        const uint32_t pos0 = start + t * kTile + 4u * grp;
-        float sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float v;
-            {
+            for (int h = 0; h < 2; ++h) acc[m][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        while (have && lc == c) {
+            const uint32_t j = lj;
+            uint32_t nc = lc, nj = lj;
+            const bool has_next = advance(nc, nj);
+            Tile nxt;
+            if (has_next) load_tile(nxt, nc, nj);
+            if (PH0 && owner && min(cstart + j * kTile + tok, cend) == limit) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    cur.k[m] = *reinterpret_cast<const uint4*>(&s_fresh[32u * m + 8u * grp]);
+                    cur.v[m] =
+                        *reinterpret_cast<const uint4*>(&s_fresh[128u + 32u * m + 8u * grp]);
+                }
+            }
+
+            // S^T = K x Q^T
+            f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.k[m]), qb[m], s,
+                                                            0, 0, 0);
+            const uint32_t pos0 = cstart + j * kTile + 4u * grp;
+            float sc[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                float v;
+                {
 #pragma clang fp contract(off)
-                v = s[j] * kScoreScale;
+                    v = s[jj] * kScoreScale;
+                }
+                sc[jj] = (pos0 + (uint32_t)jj <= cend) ? v : -INFINITY;
             }
-            sc[j] = (pos0 + (uint32_t)j <= end) ? v : -INFINITY;
-        }
-        float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        tm = fmaxf(tm, __shfl_xor(tm, 16));
-        tm = fmaxf(tm, __shfl_xor(tm, 32));
-        const float mn = fmaxf(m_run, tm);
-        const float renew = (m_run == -INFINITY) ? 0.f : __expf(m_run - mn);
-        float p[4];
+            float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            tm = fmaxf(tm, __shfl_xor(tm, 16));
+            tm = fmaxf(tm, __shfl_xor(tm, 32));
+            const float mn = fmaxf(m_run, tm);
+            const float renew = (m_run == -INFINITY) ? 0.f : __expf(m_run - mn);
+            float p[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = __expf(sc[j] - mn);
-        float ls = (p[0] + p[1]) + (p[2] + p[3]);
-        ls += __shfl_xor(ls, 16);
-        ls += __shfl_xor(ls, 32);
-        l_run = l_run * renew + ls;
-        m_run = mn;
-        s16x4 pb;
+            for (int jj = 0; jj < 4; ++jj) p[jj] = __expf(sc[jj] - mn);
+            float ls = (p[0] + p[1]) + (p[2] + p[3]);
+            ls += __shfl_xor(ls, 16);
+            ls += __shfl_xor(ls, 32);
+            l_run = l_run * renew + ls;
+            m_run = mn;
+            s16x4 pb;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pb[j] = (short)f32_to_bf16(p[j]);
+            for (int jj = 0; jj < 4; ++jj) pb[jj] = (short)f32_to_bf16(p[jj]);
 
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+            for (int m = 0; m < 4; ++m)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                const f32x4 vt = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                    half_s16x4(cur.v[m], h), ident, z, 0, 0, 0);
-                acc[m][h] = acc[m][h] * renew;
-                acc[m][h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                    trunc_bf16x4(vt), pb, acc[m][h], 0, 0, 0);
-            }
-        if (has_next) cur = nxt;
-    }
+                for (int h = 0; h < 2; ++h) {
+                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    const f32x4 vt = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        half_s16x4(cur.v[m], h), ident, z, 0, 0, 0);
+                    acc[m][h] = acc[m][h] * renew;
+                    acc[m][h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        trunc_bf16x4(vt), pb, acc[m][h], 0, 0, 0);
+                }
+            have = has_next;
+            lc = nc;
+            lj = nj;
+            if (has_next) cur = nxt;
+        }
 
-    // Fold the 4 wave states (fixed wave order) through LDS.
-    if (tok < kGroup) {
-        if (grp == 0u) {
-            s_m[wave][tok] = m_run;
-            s_l[wave][tok] = l_run;
+        // Fold the 4 wave states of chunk c (fixed wave order) through LDS.
+        const uint32_t b = c & 1u;
+        if (tok < kGroup) {
+            if (grp == 0u) {
+                s_m[b][wave][tok] = m_run;
+                s_l[b][wave][tok] = l_run;
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    *reinterpret_cast<f32x4*>(
+                        &s_acc[b][wave][tok][32u * m + 8u * grp + 4u * h]) = acc[m][h];
         }
+        __syncthreads();
+        const uint32_t head = tid >> 5;        // 0..7
+        const uint32_t d4 = (tid & 31u) * 4u;  // 4 dims
+        float M = -INFINITY;
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (uint32_t w = 0; w < kWaves; ++w)
+            if (s_l[b][w][head] != 0.f) M = fmaxf(M, s_m[b][w][head]);
+        float L = 0.f;
+        f32x4 A = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                *reinterpret_cast<f32x4*>(&s_acc[wave][tok][32u * m + 8u * grp + 4u * h]) =
-                    acc[m][h];
-    }
-    __syncthreads();
-    const uint32_t head = tid >> 5;         // 0..7
-    const uint32_t d4 = (tid & 31u) * 4u;   // 4 dims
-    float M = -INFINITY;
-#pragma unroll
-    for (uint32_t w = 0; w < kWaves; ++w)
-        if (s_l[w][head] != 0.f) M = fmaxf(M, s_m[w][head]);
-    float L = 0.f;
-    f32x4 A = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (uint32_t w = 0; w < kWaves; ++w) {
-        const float lw = s_l[w][head];
-        if (lw == 0.f) continue;
-        const float f = __expf(s_m[w][head] - M);
-        L += lw * f;
-        A += *reinterpret_cast<const f32x4*>(&s_acc[w][head][d4]) * f;
-    }
-    const uint32_t qh = kvh * kGroup + head;
-    if (limit < C) {
-        uint16_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(L > 0.f ? A[i] / L : 0.f);
-        *reinterpret_cast<uint2*>(a.out + qh * kD + d4) =
-            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
-                       (uint32_t)o[2] | ((uint32_t)o[3] << 16));
-    } else {
-        float* pw = a.partials + ((size_t)qh * NC + chunk) * kPartial;
-        if (d4 == 0u) {
-            pw[0] = M;
-            pw[1] = L;
+        for (uint32_t w = 0; w < kWaves; ++w) {
+            const float lw = s_l[b][w][head];
+            if (lw == 0.f) continue;
+            const float f = __expf(s_m[b][w][head] - M);
+            L += lw * f;
+            A += *reinterpret_cast<const f32x4*>(&s_acc[b][w][head][d4]) * f;
         }
-        *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(A[0], A[1]);
-        *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(A[2], A[3]);
+        const uint32_t qh = kvh * kGroup + head;
+        if (limit < C) {
+            uint16_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(L > 0.f ? A[i] / L : 0.f);
+            *reinterpret_cast<uint2*>(a.out + qh * kD + d4) =
+                make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
+                           (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+        } else {
+            float* pw = a.partials + ((size_t)qh * NC + c) * kPartial;
+            if (d4 == 0u) {
+                pw[0] = M;
+                pw[1] = L;
+            }
+            *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(A[0], A[1]);
+            *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(A[2], A[3]);
+        }
     }
 }
 
-// grid = (NC, 2 kv heads, B slots). Single-session launches pass B = 1 and the
-// direct pointers; batched launches resolve per-slot pointers from tables.
+#if MCKV_WAVES_PER_EU
+#define MCKV_CHUNK_ATTR __attribute__((amdgpu_waves_per_eu(MCKV_WAVES_PER_EU)))
+#else
+#define MCKV_CHUNK_ATTR
+#endif
+// grid = (ceil(NC / cpw), 2 kv heads, B slots). Single-session launches pass
+// B = 1 and the direct pointers; batched launches resolve per-slot pointers
+// from device tables.
 template <bool PH0, bool BATCH>
-__global__ void __launch_bounds__(kThreads) decode_chunk_kernel(
+__global__ void __launch_bounds__(kThreads) MCKV_CHUNK_ATTR decode_chunk_kernel(
     const uint16_t* __restrict__ q_rows, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t layer,
     const uint32_t* pt, const uint32_t* const* __restrict__ slot_pt,
     uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
     float* __restrict__ partials, uint32_t NC, uint16_t* __restrict__ out,
-    const float* __restrict__ inv_freq, uint32_t C) {
+    const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw) {
     const uint32_t slot = blockIdx.z;
     DecodeArgs a;
     a.q_row = q_rows + (size_t)slot * kRow;
@@ -353,13 +397,59 @@ __global__ void __launch_bounds__(kThreads) decode_chunk_kernel(
     a.pool = BATCH ? slot_kv[slot] : pool;
     a.partials = partials + (size_t)slot * kHq * NC * kPartial;
     a.out = out + (size_t)slot * kHq * kD;
-    decode_chunk_body<PH0>(a, layer, ly, NC, inv_freq, C, blockIdx.y, blockIdx.x);
+    decode_range_body<PH0>(a, layer, ly, NC, inv_freq, C, blockIdx.y, blockIdx.x * cpw, cpw);
 }
 
 __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
                                                    uint32_t NC) {
     const uint32_t n = limit / C + 1u;
     return n > NC ? NC : n;
+}
+
+constexpr uint32_t kMaxFold = 2048;  // partials folded by one 128-thread block
+
+// Folds n partials {m, l, acc[128]} at base + i*stride (i ascending) with the
+// reference merge rule: M = max m over l != 0; f_i = exp(m_i - M);
+// L = sum l_i f_i; A[d] = sum acc_i[d] f_i (ascending, l == 0 skipped). The
+// (m, l) pairs are loaded by all threads at once and the acc loads are
+// independent, so the fold costs a few memory latencies instead of n.
+// Block = 128 threads, thread = dim. Returns A for dim threadIdx.x; M, L
+// through references. n <= kMaxFold.
+__device__ __forceinline__ float fold_partials(const float* __restrict__ base,
+                                               size_t stride, uint32_t n, float& M_out,
+                                               float& L_out) {
+    __shared__ float s_m[kMaxFold], s_l[kMaxFold], s_red[4];
+    const uint32_t d = threadIdx.x;
+    float mx = -INFINITY;
+    for (uint32_t i = d; i < n; i += 128u) {
+        const float2 ml = *reinterpret_cast<const float2*>(base + i * stride);
+        s_m[i] = ml.x;
+        s_l[i] = ml.y;
+        if (ml.y != 0.f) mx = fmaxf(mx, ml.x);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((d & 63u) == 0u) s_red[d >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(s_red[0], s_red[1]);
+    for (uint32_t i = d; i < n; i += 128u)
+        s_m[i] = (s_l[i] != 0.f) ? expf(s_m[i] - M) : 0.f;  // s_m now holds f_i
+    __syncthreads();
+    // Branch-free accumulation: every load is issued unconditionally (the
+    // select keeps an l == 0 partial, whatever its acc holds, out of the sum),
+    // so 16 loads are in flight at once.
+    float L = 0.f, A = 0.f;
+#pragma unroll 16
+    for (uint32_t i = 0; i < n; ++i) {
+        const float v = base[i * stride + 2u + d];
+        const float f = s_m[i];
+        const bool live = s_l[i] != 0.f;
+        L += live ? s_l[i] * f : 0.f;
+        A += live ? v * f : 0.f;
+    }
+    M_out = M;
+    L_out = L;
+    return A;
 }
 
 // Level-1 -> level-2 merge. grid = (B*16, 32), block = 128 (thread = dim).
@@ -373,7 +463,6 @@ __global__ void __launch_bounds__(128) merge_a_kernel(
     const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
     const uint32_t nv = n_valid_chunks(limit, C, NC);
     if (nv == 1u) return;
-    const float* P = partials + ((size_t)slot * kHq + qh) * NC * kPartial;
     float* pw2 = partials2 + (((size_t)slot * kHq + qh) * kSplit2 + s) * kPartial;
     if (s >= nv) {
         if (d == 0u) {
@@ -382,43 +471,15 @@ __global__ void __launch_bounds__(128) merge_a_kernel(
         }
         return;
     }
-    float mloc = -INFINITY;
-    for (uint32_t c = s; c < nv; c += kSplit2) {
-        const float* p = P + (size_t)c * kPartial;
-        if (p[1] != 0.f) mloc = fmaxf(mloc, p[0]);
-    }
-    float L = 0.f, A = 0.f;
-    for (uint32_t c = s; c < nv; c += kSplit2) {
-        const float* p = P + (size_t)c * kPartial;
-        if (p[1] == 0.f) continue;
-        const float f = expf(p[0] - mloc);
-        L += p[1] * f;
-        A += p[2 + d] * f;
-    }
+    const float* P = partials + (((size_t)slot * kHq + qh) * NC + s) * kPartial;
+    float M, L;
+    const float A = fold_partials(P, (size_t)kSplit2 * kPartial, (nv - s + kSplit2 - 1u) / kSplit2,
+                                  M, L);
     if (d == 0u) {
-        pw2[0] = mloc;
+        pw2[0] = M;
         pw2[1] = L;
     }
     pw2[2 + d] = A;
-}
-
-// Fold of `n` partials with stride kPartial (fixed ascending order) -> bf16.
-__device__ __forceinline__ void fold_to_out(const float* __restrict__ P, uint32_t n,
-                                            uint32_t d, uint16_t* __restrict__ o) {
-    float M = -INFINITY;
-    for (uint32_t i = 0; i < n; ++i) {
-        const float* p = P + (size_t)i * kPartial;
-        if (p[1] != 0.f) M = fmaxf(M, p[0]);
-    }
-    float L = 0.f, A = 0.f;
-    for (uint32_t i = 0; i < n; ++i) {
-        const float* p = P + (size_t)i * kPartial;
-        if (p[1] == 0.f) continue;
-        const float f = expf(p[0] - M);
-        L += p[1] * f;
-        A += p[2 + d] * f;
-    }
-    *o = f32_to_bf16(L > 0.f ? A / L : 0.f);
 }
 
 // Level-2 -> out. grid = B*16, block = 128.
@@ -430,12 +491,14 @@ __global__ void __launch_bounds__(128) merge_b_kernel(
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
     const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
     if (n_valid_chunks(limit, C, NC) == 1u) return;
-    fold_to_out(partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial, kSplit2,
-                threadIdx.x, out + ((size_t)slot * kHq + qh) * kD + threadIdx.x);
+    float M, L;
+    const float A = fold_partials(partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial,
+                                  kPartial, kSplit2, M, L);
+    out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
 }
 
 // One-level merge of all valid level-1 partials (used when no level-2 buffer
-// is given). grid = B*16, block = 128.
+// is given). grid = B*16, block = 128; the fold runs in pieces of kMaxFold.
 template <bool BATCH>
 __global__ void __launch_bounds__(128) merge_p_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
@@ -445,8 +508,23 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
     const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
     const uint32_t nv = n_valid_chunks(limit, C, NC);
     if (nv == 1u) return;
-    fold_to_out(partials + ((size_t)slot * kHq + qh) * NC * kPartial, nv, threadIdx.x,
-                out + ((size_t)slot * kHq + qh) * kD + threadIdx.x);
+    float M, L;
+    const float A = fold_partials(partials + ((size_t)slot * kHq + qh) * NC * kPartial,
+                                  kPartial, nv, M, L);
+    out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
+}
+
+// Chunks per workgroup: enough workgroups for ~kTargetBlocks resident blocks
+// (2 per CU on 256 CUs) when there are more chunks than that; C % 64 == 0 is
+// needed for cpw > 1 (all 4 waves then cross chunk boundaries together).
+#ifndef MCKV_TARGET_BLOCKS
+#define MCKV_TARGET_BLOCKS 512
+#endif
+uint32_t chunks_per_block(uint32_t NC, uint32_t B, uint32_t C) {
+    if (C % 64u != 0u) return 1u;
+    const uint32_t units = NC * kHkv * B;
+    const uint32_t cpw = units / MCKV_TARGET_BLOCKS;
+    return cpw < 1u ? 1u : cpw;
 }
 
 template <bool BATCH>
@@ -456,15 +534,16 @@ mc_status_t launch_chunks(const uint16_t* q, const uint32_t* d_pos,
                           uint16_t* pool, uint16_t* const* slot_kv, DevLayout ly,
                           float* partials, uint32_t NC, uint16_t* out,
                           hipStream_t st, const float* inv_freq, uint32_t C) {
-    const dim3 grid(NC, kHkv, B);
+    const uint32_t cpw = chunks_per_block(NC, B, C);
+    const dim3 grid((NC + cpw - 1u) / cpw, kHkv, B);
     if (inv_freq != nullptr)
         hipLaunchKernelGGL((decode_chunk_kernel<true, BATCH>), grid, dim3(kThreads), 0,
                            st, q, d_pos, slot_pos, layer, pt, slot_pt, pool, slot_kv, ly,
-                           partials, NC, out, inv_freq, C);
+                           partials, NC, out, inv_freq, C, cpw);
     else
         hipLaunchKernelGGL((decode_chunk_kernel<false, BATCH>), grid, dim3(kThreads),
                            0, st, q, d_pos, slot_pos, layer, pt, slot_pt, pool, slot_kv,
-                           ly, partials, NC, out, inv_freq, C);
+                           ly, partials, NC, out, inv_freq, C, cpw);
     return check_launch("decode attention chunk launch failed");
 }
 
@@ -485,7 +564,7 @@ mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
 }
 
 bool chunk_args_ok(uint32_t max_chunks, uint32_t chunk_pos) {
-    return max_chunks > 0 && max_chunks <= 65535u && chunk_pos >= 16u &&
+    return max_chunks > 0 && max_chunks <= kMaxFold && chunk_pos >= 16u &&
            chunk_pos % 16u == 0u;
 }
 

@@ -10,3 +10,15 @@ namespace mckv {
 bool layout_valid(const mc_kv_layout_t& l, DevLayout* out);
 
 }  // namespace mckv
+
+namespace mckv {
+
+// Deterministic synthetic qkv rows (synth.hip).
+mc_status_t launch_synth_qkv(uint16_t* rows, uint32_t n, const int32_t* tokens,
+                             const uint32_t* base_pos, uint32_t layer, hipStream_t st);
+mc_status_t launch_synth_qkv_batch(uint16_t* rows, uint32_t n,
+                                   const int32_t* const* slot_tok,
+                                   const uint32_t* const* slot_pos, uint32_t layer,
+                                   hipStream_t st);
+
+}  // namespace mckv

@@ -1,0 +1,191 @@
+"""Python binding of the mc_* session ABI (include/minicpm_runtime.h).
+
+Mirrors what the reference's Rust wrapper does over dlopen
+(rust/minicpm-runtime/src/native.rs:42-94,386-525): POD option structs with
+struct_size/abi_version, by-value opaque handles, mc_last_error() on failure.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+from ._native import McError, check, lib, LayoutT
+
+MC_ABI_VERSION = 0x00020000
+EOS_STREAM_ID = 130073
+
+
+class ModelOptions(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_version", C.c_uint32),
+                ("device_id", C.c_int32), ("max_sessions", C.c_uint32),
+                ("max_context_tokens", C.c_uint32), ("precision", C.c_int),
+                ("kv_precision", C.c_int), ("enable_cuda_graph", C.c_uint32),
+                ("reserve_vram_bytes", C.c_uint64)]
+
+
+class GenerationConfig(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("max_new_tokens", C.c_uint32),
+                ("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+                ("repetition_penalty", C.c_float), ("seed", C.c_uint64)]
+
+
+class RuntimeStats(C.Structure):
+    _fields_ = [("prompt_tokens", C.c_uint64), ("generated_tokens", C.c_uint64),
+                ("prefill_us", C.c_uint64), ("decode_us", C.c_uint64),
+                ("peak_vram_bytes", C.c_uint64), ("cuda_graph_launches", C.c_uint64)]
+
+
+class BatchOptions(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_version", C.c_uint32),
+                ("max_slots", C.c_uint32), ("max_context_tokens", C.c_uint32),
+                ("reserved", C.c_uint32 * 4)]
+
+
+class Handle(C.Structure):
+    _fields_ = [("impl", C.c_void_p)]
+
+
+assert C.sizeof(ModelOptions) == 40 and C.sizeof(GenerationConfig) == 32
+assert C.sizeof(BatchOptions) == 32
+
+_P = C.c_void_p
+_bound = False
+
+
+def _bind():
+    global _bound
+    if _bound:
+        return lib()
+    L = lib()
+    sig = {
+        "mc_model_load": (C.c_int, [C.c_char_p, C.POINTER(ModelOptions), C.POINTER(Handle)]),
+        "mc_model_destroy": (None, [Handle]),
+        "mc_session_create": (C.c_int, [Handle, C.POINTER(Handle)]),
+        "mc_session_reset": (C.c_int, [Handle]),
+        "mc_session_destroy": (None, [Handle]),
+        "mc_prefill": (C.c_int, [Handle, C.POINTER(C.c_int32), C.c_uint32]),
+        "mc_decode_one": (C.c_int, [Handle, C.POINTER(GenerationConfig),
+                                    C.POINTER(C.c_int32)]),
+        "mc_get_stats": (C.c_int, [Handle, C.POINTER(RuntimeStats)]),
+        "mc_batch_group_create": (C.c_int, [Handle, C.POINTER(BatchOptions),
+                                            C.POINTER(Handle)]),
+        "mc_batch_group_add": (C.c_int, [Handle, Handle, C.POINTER(C.c_uint32)]),
+        "mc_batch_group_remove": (C.c_int, [Handle, C.c_uint32]),
+        "mc_batch_step": (C.c_int, [Handle, C.POINTER(C.c_uint32), C.c_uint32,
+                                    C.POINTER(GenerationConfig), C.POINTER(C.c_int32)]),
+        "mc_batch_group_destroy": (None, [Handle]),
+        "mc_debug_session_info": (C.c_int, [Handle, C.POINTER(C.c_uint32),
+                                            C.POINTER(C.c_uint32), C.POINTER(LayoutT),
+                                            C.POINTER(_P), C.POINTER(_P)]),
+        "mc_debug_session_seq": (C.c_int, [Handle, C.POINTER(C.c_int32), C.c_uint32]),
+    }
+    for n, (r, a) in sig.items():
+        f = getattr(L, n)
+        f.restype, f.argtypes = r, a
+    _bound = True
+    return L
+
+
+def model_options(max_context_tokens=2048, max_sessions=4, device_id=0, **kw) -> ModelOptions:
+    o = ModelOptions(C.sizeof(ModelOptions), MC_ABI_VERSION, device_id, max_sessions,
+                     max_context_tokens, 0, 0, 0, 0)
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+def gen_config(max_new_tokens=64, temperature=0.0, top_k=1, seed=0, **kw) -> GenerationConfig:
+    c = GenerationConfig(C.sizeof(GenerationConfig), max_new_tokens, temperature, 1.0, top_k,
+                         1.0, seed)
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+class Model:
+    def __init__(self, model_dir: str, options: ModelOptions):
+        L = _bind()
+        self.h = Handle()
+        check(L.mc_model_load(model_dir.encode(), C.byref(options), C.byref(self.h)),
+              "mc_model_load")
+
+    def close(self):
+        if self.h.impl:
+            _bind().mc_model_destroy(self.h)
+            self.h = Handle()
+
+
+class Session:
+    def __init__(self, model: Model):
+        L = _bind()
+        self.h = Handle()
+        check(L.mc_session_create(model.h, C.byref(self.h)), "mc_session_create")
+
+    def prefill(self, tokens) -> None:
+        arr = (C.c_int32 * len(tokens))(*tokens)
+        check(_bind().mc_prefill(self.h, arr, len(tokens)), "mc_prefill")
+
+    def decode_one(self, cfg: GenerationConfig) -> int:
+        out = C.c_int32()
+        check(_bind().mc_decode_one(self.h, C.byref(cfg), C.byref(out)), "mc_decode_one")
+        return out.value
+
+    def reset(self) -> None:
+        check(_bind().mc_session_reset(self.h), "mc_session_reset")
+
+    def stats(self) -> RuntimeStats:
+        st = RuntimeStats()
+        check(_bind().mc_get_stats(self.h, C.byref(st)), "mc_get_stats")
+        return st
+
+    def info(self):
+        seq, pages, lay, pool, pt = C.c_uint32(), C.c_uint32(), LayoutT(), _P(), _P()
+        check(_bind().mc_debug_session_info(self.h, C.byref(seq), C.byref(pages),
+                                            C.byref(lay), C.byref(pool), C.byref(pt)),
+              "mc_debug_session_info")
+        return {"seq_len": seq.value, "pages_owned": pages.value, "layout": lay,
+                "d_pool": pool.value, "d_page_table": pt.value}
+
+    def seq(self, n: int):
+        out = (C.c_int32 * n)()
+        check(_bind().mc_debug_session_seq(self.h, out, n), "mc_debug_session_seq")
+        return list(out)
+
+    def close(self):
+        if self.h.impl:
+            _bind().mc_session_destroy(self.h)
+            self.h = Handle()
+
+
+class BatchGroup:
+    def __init__(self, model: Model, max_slots: int, max_context_tokens: int, reserved=None):
+        L = _bind()
+        o = BatchOptions(C.sizeof(BatchOptions), MC_ABI_VERSION, max_slots,
+                         max_context_tokens, (C.c_uint32 * 4)(*(reserved or [0, 0, 0, 0])))
+        self.h = Handle()
+        check(L.mc_batch_group_create(model.h, C.byref(o), C.byref(self.h)),
+              "mc_batch_group_create")
+
+    def add(self, s: Session) -> int:
+        slot = C.c_uint32()
+        check(_bind().mc_batch_group_add(self.h, s.h, C.byref(slot)), "mc_batch_group_add")
+        return slot.value
+
+    def remove(self, slot: int) -> None:
+        check(_bind().mc_batch_group_remove(self.h, slot), "mc_batch_group_remove")
+
+    def step(self, slots, cfgs):
+        n = len(slots)
+        ids = (C.c_uint32 * n)(*slots)
+        cf = (GenerationConfig * n)(*cfgs)
+        out = (C.c_int32 * n)()
+        check(_bind().mc_batch_step(self.h, ids, n, cf, out), "mc_batch_step")
+        return list(out)
+
+    def close(self):
+        if self.h.impl:
+            _bind().mc_batch_group_destroy(self.h)
+            self.h = Handle()
+
+
+__all__ = ["Model", "Session", "BatchGroup", "model_options", "gen_config", "McError",
+           "EOS_STREAM_ID"]

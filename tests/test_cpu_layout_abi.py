@@ -1,0 +1,88 @@
+"""CPU tests: pool addressing and tier tables against the reference's
+known-answer literals (tests/golden/kv_addressing.json), and the exported
+C ABI of libminicpm_native.so (every function declared in include/*.h)."""
+import json
+import os
+import re
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+GOLD = json.load(open(os.path.join(HERE, "golden", "kv_addressing.json")))
+
+
+def test_elem_offset_literals_product(kvm):
+    lay = kvm.KvLayout(GOLD["max_pages"], GOLD["tokens_per_page"], GOLD["num_layers"])
+    for l, p, s, kv, h, d, want in GOLD["elem_offset"]:
+        assert lay.elem_offset(l, p, s, kv, h, d) == want
+    assert lay.total_elems() == GOLD["total_elems"]
+    for pos, page, slot in GOLD["pos_to_page_slot"]:
+        assert lay.page_index(pos) == page and lay.slot_index(pos) == slot
+
+
+def test_elem_offset_literals_oracle(orc):
+    for l, p, s, kv, h, d, want in GOLD["elem_offset"]:
+        assert orc.kv_off(32, 256, l, p, s, kv, h, d) == want
+
+
+def test_elem_offset_formula_general(kvm, orc):
+    """Product == oracle for other page sizes / layer counts (P=64, L=28)."""
+    for P in (1, 16, 32, 64, 128):
+        for mp in (1, 8, 2048):
+            lay = kvm.KvLayout(mp, P, 28)
+            for l in (0, 13, 27):
+                for page in (0, mp - 1):
+                    for slot in (0, P - 1):
+                        for kv in (0, 1):
+                            for h in (0, 1):
+                                for d in (0, 127):
+                                    assert lay.elem_offset(l, page, slot, kv, h, d) == \
+                                        orc.kv_off(P, mp, l, page, slot, kv, h, d)
+            assert lay.total_elems() == mp * P * 512 * 28
+
+
+def test_bad_layout_rejected(pkg):
+    L = pkg._native
+    assert L.lib().mc_kv_total_elems(L.layout(8, 48, 2)) == 0  # P not a power of two
+    assert L.lib().mc_kv_elem_offset(L.layout(0, 32, 2), 0, 0, 0, 0, 0, 0) == 2 ** 64 - 1
+
+
+def test_tier_tables(kvm, orc):
+    for ctx, c in GOLD["chunk_pos_tiers"]:
+        assert kvm.attention_decode_chunk_pos(ctx) == c == orc.chunk_pos(ctx)
+    assert kvm.attention_decode_max_chunks(131072, 256) == 512
+    assert kvm.attention_decode_max_chunks(8448, 64) == 132
+    for t, s in GOLD["prefill_split_kv"]:
+        assert kvm.prefill_flash_split_kv(t) == s == orc.prefill_split_kv(t)
+
+
+def _declared(header):
+    txt = open(os.path.join(ROOT, "include", header)).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(mc_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_all_declared_symbols_exported(pkg):
+    import ctypes
+    lib = ctypes.CDLL(pkg._native.LIB_PATH)
+    names = _declared("minicpm_runtime.h") + _declared("mc_kv.h")
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_error_convention(pkg, kvm):
+    """Invalid arguments return MC_E_INVALID_ARGUMENT with a message and no
+    device work (runs without a GPU)."""
+    with pytest.raises(pkg.McError) as e:
+        kvm.launch_attention_decode(None, None, 0, None, None, kvm.KvLayout(8, 32, 1), None,
+                                    12, None, stream=0)
+    assert e.value.status == 1 and "invalid args" in str(e.value)
+    with pytest.raises(pkg.McError) as e:
+        kvm.launch_attn_prefill_flash(None, 0, None, 0, None, None, kvm.KvLayout(8, 32, 1),
+                                      None, None, 9, stream=0)
+    assert e.value.status == 1
+    with pytest.raises(pkg.McError):
+        kvm.launch_rope_kv(None, 1, None, 0, None, None, kvm.KvLayout(8, 32, 1), 5e6,
+                           stream=0)

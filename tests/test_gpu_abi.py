@@ -1,0 +1,259 @@
+"""GPU tests of the mc_* ABI shell (weight-free mode) driving the KV path:
+option/handle validation (model.cpp, batch_group.cpp rules), prefill ->
+pages + RoPE'd K/V in the pool, decode -> mock token rule + phase0 append,
+reset, OOM, max_new_tokens sentinel, and batched steps equal to solo steps
+(tokens, sequences and pool bytes), after batch_test.cpp scenarios A/B.
+
+The synthetic qkv rows of the weight-free runtime are restated here (the hash
+of synth.hip) so pool contents can be checked against the oracle's kernel-
+exact RoPE append."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+P, L, THETA = 32, 42, 5e6
+M32 = 0xFFFFFFFF
+
+
+def mix32(x):
+    x = np.asarray(x, dtype=np.uint64) & M32
+    x ^= x >> 16
+    x = (x * 0x85EBCA6B) & M32
+    x ^= x >> 13
+    x = (x * 0xC2B2AE35) & M32
+    x ^= x >> 16
+    return x
+
+
+def synth_row(orc, tok, pos, layer):
+    seed = mix32(((tok * 0x9E3779B1) & M32) ^ int(mix32(pos + 0x632BE5AB)) ^
+                 ((layer * 0x85EBCA77) & M32))
+    h = mix32(seed ^ ((np.arange(2560, dtype=np.uint64) * 0x27D4EB2F) & M32))
+    u = (h >> 8).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    return orc.f32_to_bf16(u - np.float32(0.5))
+
+
+def mock_token(seq_len, rng):
+    return 100 + (((seq_len * 2654435761) & M32) ^ rng) % 1000
+
+
+def xorshift32(x):
+    x ^= (x << 13) & M32
+    x ^= x >> 17
+    x ^= (x << 5) & M32
+    return x & M32
+
+
+_hip = None
+
+
+def d2h(ptr, nbytes, dtype):
+    global _hip
+    if _hip is None:
+        _hip = C.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        _hip.hipDeviceSynchronize.argtypes = []
+    out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype=dtype)
+    assert _hip.hipMemcpy(out.ctypes.data, ptr, nbytes, 2) == 0
+    return out
+
+
+@pytest.fixture(scope="module")
+def rt(pkg, dev):
+    import importlib
+    return importlib.import_module("minicpm5-5080fast_amd.runtime")
+
+
+@pytest.fixture()
+def model(rt, tmp_path):
+    m = rt.Model(str(tmp_path), rt.model_options(max_context_tokens=2048, max_sessions=8))
+    yield m
+    m.close()
+
+
+def test_model_load_validation(rt, tmp_path):
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(tmp_path), rt.model_options(struct_size=36))
+    assert e.value.status == 1
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(tmp_path / "missing"), rt.model_options())
+    assert e.value.status == 2
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(tmp_path), rt.model_options(max_context_tokens=0))
+    assert e.value.status == 7
+    (tmp_path / "model.wpk").write_bytes(b"x")
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(tmp_path), rt.model_options())
+    assert e.value.status == 7 and "weight" in str(e.value)
+
+
+def pool_token(info, layer, pos, pt):
+    lay = info["layout"]
+    off = (((layer * lay.max_pages + int(pt[pos // P])) * P) + pos % P) * 512
+    return d2h(info["d_pool"] + off * 2, 1024, np.uint16)
+
+
+def test_prefill_decode_reset(rt, model, orc):
+    s = rt.Session(model)
+    prompt = [int(x) for x in np.random.default_rng(1).integers(0, 130560, 300)]
+    s.prefill(prompt)
+    info = s.info()
+    assert info["seq_len"] == 300 and info["pages_owned"] == 10
+    pt = d2h(info["d_page_table"], 40, np.uint32)
+    assert pt.tolist() == list(range(10))
+    lay = info["layout"]
+    # K/V of a few prompt positions in two layers == kernel-exact oracle
+    for layer in (0, 41):
+        for pos in (0, 31, 32, 299):
+            row = synth_row(orc, prompt[pos], pos, layer).reshape(1, 2560)
+            pool = np.zeros(lay.max_pages * P * 512 * L, np.uint16)
+            orc.rope_append(row, 1, pos, layer, pt, P, lay.max_pages, THETA, 1, pool)
+            off = orc.kv_off(P, lay.max_pages, layer, int(pt[pos // P]), pos % P, 0, 0, 0)
+            assert np.array_equal(pool_token(info, layer, pos, pt), pool[off:off + 512])
+    cfg = rt.gen_config(max_new_tokens=6, seed=1234)
+    rng, toks = 1234, []
+    for i in range(6):
+        want = mock_token(300 + i, rng)
+        rng = xorshift32(rng)
+        got = s.decode_one(cfg)
+        assert got == want
+        toks.append(got)
+    assert s.decode_one(cfg) == rt.EOS_STREAM_ID  # max_new_tokens sentinel
+    info = s.info()
+    assert info["seq_len"] == 306 and info["pages_owned"] == 10
+    assert s.seq(306) == prompt + toks
+    # phase0 appended K/V of decode positions: input token = previous token
+    pt = d2h(info["d_page_table"], 40, np.uint32)
+    prev = [prompt[-1]] + toks
+    for i, pos in enumerate(range(300, 306)):
+        row = synth_row(orc, prev[i], pos, 7).reshape(1, 2560)
+        pool = np.zeros(lay.max_pages * P * 512 * L, np.uint16)
+        orc.rope_append(row, 1, pos, 7, pt, P, lay.max_pages, THETA, 1, pool)
+        off = orc.kv_off(P, lay.max_pages, 7, int(pt[pos // P]), pos % P, 0, 0, 0)
+        assert np.array_equal(pool_token(info, 7, pos, pt), pool[off:off + 512])
+    st = s.stats()
+    assert st.prompt_tokens == 300 and st.generated_tokens == 6
+    s.reset()
+    assert s.info()["seq_len"] == 0 and s.info()["pages_owned"] == 0
+    s.prefill(prompt[:40])
+    assert s.info()["pages_owned"] == 2
+    with pytest.raises(rt.McError) as e:
+        s.prefill([1] * 2048)
+    assert e.value.status == 5
+    s.close()
+
+
+def test_decode_errors(rt, model):
+    s = rt.Session(model)
+    with pytest.raises(rt.McError) as e:
+        s.decode_one(rt.gen_config())
+    assert e.value.status == 1  # empty sequence
+    with pytest.raises(rt.McError) as e:
+        s.prefill([130560])
+    assert e.value.status == 1
+    s.prefill([5, 6, 7])
+    with pytest.raises(rt.McError) as e:
+        s.decode_one(rt.gen_config(struct_size=28))
+    assert e.value.status == 1
+    s.close()
+
+
+def test_batch_equals_solo(rt, model):
+    """Scenario A/B of batch_test.cpp: tokens from batched steps equal solo
+    decode, and the KV pools end bit-identical."""
+    rng = np.random.default_rng(7)
+    prompts = [[int(x) for x in rng.integers(0, 130560, n)] for n in (100, 333, 64)]
+    solo = [rt.Session(model) for _ in prompts]
+    bat = [rt.Session(model) for _ in prompts]
+    for a, b, p in zip(solo, bat, prompts):
+        a.prefill(p)
+        b.prefill(p)
+    cfgs = [rt.gen_config(max_new_tokens=100, seed=11 * (i + 1)) for i in range(3)]
+    want = [[a.decode_one(cfgs[i]) for _ in range(5)] for i, a in enumerate(solo)]
+    g = rt.BatchGroup(model, 4, 2048)
+    slots = [g.add(b) for b in bat]
+    got = [[] for _ in bat]
+    for step in range(5):
+        out = g.step(slots, cfgs)
+        for i, t in enumerate(out):
+            got[i].append(t)
+    assert got == want
+    for s_ in slots:
+        g.remove(s_)
+    for a, b, p in zip(solo, bat, prompts):
+        ia, ib = a.info(), b.info()
+        assert ia["seq_len"] == ib["seq_len"] == len(p) + 5
+        nb = ia["pages_owned"] * P * 1024
+        lay = ia["layout"]
+        for layer in (0, 20, 41):
+            base = layer * lay.max_pages * P * 1024
+            assert np.array_equal(d2h(ia["d_pool"] + base, nb, np.uint16),
+                                  d2h(ib["d_pool"] + base, nb, np.uint16))
+        assert a.seq(len(p) + 5) == b.seq(len(p) + 5)
+    # solo -> batch -> solo lifecycle continues consistently
+    assert bat[0].decode_one(cfgs[0]) == solo[0].decode_one(cfgs[0])
+    g.close()
+    for s_ in solo + bat:
+        s_.close()
+
+
+def test_batch_group_rules(rt, model, tmp_path):
+    with pytest.raises(rt.McError) as e:
+        rt.BatchGroup(model, 4, 2048, reserved=[0, 1, 0, 0])
+    assert e.value.status == 1
+    with pytest.raises(rt.McError) as e:
+        rt.BatchGroup(model, 9, 2048)
+    assert e.value.status == 7
+    with pytest.raises(rt.McError) as e:
+        rt.BatchGroup(model, 2, 4096)
+    assert e.value.status == 7
+    g = rt.BatchGroup(model, 2, 2048)
+    a, b, c = rt.Session(model), rt.Session(model), rt.Session(model)
+    a.prefill([1, 2, 3])
+    sa, sb = g.add(a), g.add(b)
+    with pytest.raises(rt.McError) as e:
+        g.add(c)
+    assert e.value.status == 7  # full
+    g2 = rt.BatchGroup(model, 2, 2048)
+    with pytest.raises(rt.McError) as e:
+        g2.add(a)
+    assert e.value.status == 7  # already in a group
+    cfg = rt.gen_config()
+    with pytest.raises(rt.McError) as e:
+        g.step([sa, sa], [cfg, cfg])
+    assert e.value.status == 1  # duplicate
+    with pytest.raises(rt.McError) as e:
+        g.step([sa, sb], [cfg, cfg])
+    assert e.value.status == 1  # b is empty
+    with pytest.raises(rt.McError) as e:
+        g.step([sa], [rt.gen_config(temperature=0.7, top_k=40)])
+    assert e.value.status == 7  # non-greedy
+    with pytest.raises(rt.McError) as e:
+        a.decode_one(cfg)
+    assert e.value.status == 7  # member used solo while in the group
+    with pytest.raises(rt.McError) as e:
+        g.remove(5)
+    assert e.value.status == 1
+    g.remove(sa)
+    a.decode_one(cfg)
+    g.close()
+    g2.close()
+    for s_ in (a, b, c):
+        s_.close()
+
+
+def test_session_limit(rt, tmp_path):
+    m = rt.Model(str(tmp_path), rt.model_options(max_context_tokens=256, max_sessions=2))
+    s1, s2 = rt.Session(m), rt.Session(m)
+    with pytest.raises(rt.McError) as e:
+        rt.Session(m)
+    assert e.value.status == 7
+    s1.close()
+    s3 = rt.Session(m)
+    for s_ in (s2, s3):
+        s_.close()
+    m.close()

@@ -294,3 +294,37 @@ def test_batch_vs_single_ctx600(kvm, orc, dev, B, C, ph0):
 
 def test_batch_vs_single_8x2048(kvm, orc, dev):
     _batch_case(kvm, orc, dev, 8, 64, 2047, True, seed=8)
+
+
+@pytest.mark.parametrize("ctx,C,ph0", [(40000, 64, True), (131072, 256, True),
+                                       (70001, 256, False)])
+def test_decode_long_multichunk_blocks(kvm, orc, dev, ctx, C, ph0):
+    """Long contexts where one workgroup streams several chunks (2x512+
+    chunk units), P = 64, permuted pages; phase0 appends position ctx-1."""
+    import torch
+    rng = np.random.default_rng(ctx)
+    P, L, layer = 64, 2, 1
+    maxp = -(-ctx // P) + 2
+    pt = rng.permutation(maxp).astype(np.uint32)
+    lay = kvm.KvLayout(maxp, P, L)
+    pool = np.full(lay.total_elems(), POISON, dtype=np.uint16)
+    n_fill = ctx - 1 if ph0 else ctx
+    vals = randn_bf16(rng, n_fill * 512, 0.3)
+    for j in range(n_fill):
+        base = orc.kv_off(P, maxp, layer, int(pt[j // P]), j % P, 0, 0, 0)
+        pool[base:base + 512] = vals[j * 512:(j + 1) * 512]
+    q = randn_bf16(rng, 2560, 1.0)
+    limit = ctx - 1
+    NC = -(-131072 // C)
+    inv = None
+    if ph0:
+        inv = torch.empty(64, dtype=torch.float32, device=dev)
+        kvm.launch_rope_inv_freq_init(inv, 5e6)
+    got, _, pool_after = run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, limit, C, NC,
+                                    inv=inv)
+    qkv_o, pool_o = q.reshape(1, 2560).copy(), pool.copy()
+    if ph0:
+        orc.rope_append(qkv_o, 1, limit, layer, pt, P, maxp, 5e6, 1, pool_o)
+        assert np.array_equal(pool_after, pool_o)
+    ref = orc.attn_ref(qkv_o, 1, limit, layer, pool_o, pt, P, maxp)[0]
+    check_vs_ref(orc, got, ref, f"long ctx={ctx} C={C}")

@@ -5,7 +5,12 @@ Cases follow native/tests/kernel_ops.cpp:1534-1565 (T=1 at pos 75 with table
 (8448 tokens, 64-token pages, theta 1e4 and 5e6). Criteria:
   * K, q and V bit-exact against the kernel-exact oracle (orc mode 1);
   * q/k within 2 bf16 ulp + 1e-4 of the reference's double rope_ref (mode 0),
-    V bit-exact (kernel_ops.cpp:1493-1512);
+    V bit-exact (kernel_ops.cpp:1493-1512). The reference kernel, like this one,
+    rounds the angle pos*inv_freq to fp32 (rope_kv.cu:68), which the double
+    oracle does not; the reference only tests pos < 76, where that is below
+    1e-4. For far positions the bound adds the angle rounding term
+    (|x| + |x2|) * 2^-23 * pos * inv_freq[p] (half an fp32 ulp of the angle
+    plus the rounding of inv_freq, with margin);
   * every pool element not written keeps its poison; k/v qkv columns unchanged.
 """
 import numpy as np
@@ -45,12 +50,27 @@ def run_case(kvm, orc, dev, qkv, T, base, layer, pt, P, maxp, L, theta, use_tabl
     # reference double oracle: <= 2 ulp + 1e-4 on q and K, V exact
     q0, p0 = qkv.reshape(T, 2560).copy(), pool.copy()
     orc.rope_append(q0, T, base, layer, pt, P, maxp, theta, 0, p0)
+    inv = orc.inv_freq(theta).astype(np.float64)
+    pos = (base + np.arange(T, dtype=np.float64))[:, None]
+    d = np.arange(128)
+    ang_err = 2.0 ** -23 * pos * inv[d % 64][None, :]  # [T][128]
+    src = orc.bf16_to_f32(qkv.reshape(T, 2560)[:, :2304]).astype(np.float64).reshape(T, 18, 128)
+    mag = np.abs(src) + np.abs(src[:, :, d ^ 64])
+    tol_extra = mag * ang_err[:, None, :]  # [T][18][128]
     a, r = orc.bf16_to_f32(q_got[:, :2048]), orc.bf16_to_f32(q0[:, :2048])
-    assert np.all(np.abs(a - r) <= 2 * orc.bf16_ulp(r) + 1e-4)
+    tol = 2 * orc.bf16_ulp(r) + 1e-4 + tol_extra[:, :16].reshape(T, 2048)
+    assert np.all(np.abs(a - r) <= tol)
+    k_got = np.empty((T, 256), dtype=np.uint16)
+    k_ref = np.empty((T, 256), dtype=np.uint16)
+    for t in range(T):
+        pp = base + t
+        off = orc.kv_off(P, maxp, layer, int(pt[pp // P]), pp % P, 0, 0, 0)
+        k_got[t], k_ref[t] = pool_got[off:off + 256], p0[off:off + 256]
+    ka, kr = orc.bf16_to_f32(k_got), orc.bf16_to_f32(k_ref)
+    ktol = 2 * orc.bf16_ulp(kr) + 1e-4 + tol_extra[:, 16:].reshape(T, 256)
+    assert np.all(np.abs(ka - kr) <= ktol)
     idx = np.nonzero(written)[0]
     kv = (idx % 512) // 256
-    ka, kr = orc.bf16_to_f32(pool_got[idx[kv == 0]]), orc.bf16_to_f32(p0[idx[kv == 0]])
-    assert np.all(np.abs(ka - kr) <= 2 * orc.bf16_ulp(kr) + 1e-4)
     assert np.array_equal(pool_got[idx[kv == 1]], p0[idx[kv == 1]])
 
 
