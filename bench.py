@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (eager launches)")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run one 256 MiB device copy (PMC byte calibration)")
     return ap.parse_args()
 
 
@@ -314,6 +316,13 @@ def main():
                                              args.warmup)
         log(res["c2_append_8448"])
         torch.cuda.empty_cache()
+
+    if args.calib:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        log("calibration copy: 268435456 bytes read + written")
 
     head = res.get("c4_128k")
     cpu = None if args.no_cpu or head is None else cpu_baseline(args.cpu_seconds)

@@ -121,7 +121,7 @@ struct DecodeArgs {
 // every chunk the 4 wave states are folded through LDS (double-buffered by
 // chunk parity, one barrier per chunk) and the partial (or, for a single-chunk
 // context, the output) is written. cpw > 1 requires C % 64 == 0.
-template <bool PH0>
+template <bool PH0, bool PAGE16, uint32_t TPW>
 __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t layer,
                                                   DevLayout ly, uint32_t NC,
                                                   const float* __restrict__ inv_freq,
@@ -137,7 +137,9 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     if (c_first >= nvalid) return;  // uniform over the block
     const uint32_t c_end = min(c_first + cpw, nvalid);
     const uint32_t tid = threadIdx.x;
-    const uint32_t wave = tid >> 6;
+    // Wave index made provably wave-uniform so every tile / chunk decision
+    // below compiles to scalar branches.
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lane = tid & 63u;
     const uint32_t tok = lane & 15u;  // row within a 16-position tile / head col
     const uint32_t grp = lane >> 4;   // 0..3
@@ -147,11 +149,29 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     uint16_t* __restrict__ pool = a.pool;
     const uint32_t kvcol = kvh * kD + 8u * grp;  // within a token's K or V half
 
-    auto chunk_end = [&](uint32_t c) { return min(c * C + C - 1u, limit); };
-    auto chunk_tiles = [&](uint32_t c) { return (chunk_end(c) - c * C) / kTile + 1u; };
+    // Position `limit` is kept out of the streamed tiles and added as one extra
+    // tile from LDS by wave 0 of the owning block: with phase0 its K/V come
+    // from the qkv row, otherwise from the pool. Both modes therefore run the
+    // same arithmetic (phase0 output == append-then-attend output, bitwise) and
+    // the streaming loop never patches registers.
+    const uint32_t last_pos = limit - 1u;  // last streamed position
+    auto chunk_end = [&](uint32_t c) { return min(c * C + C - 1u, last_pos); };
+    auto chunk_tiles = [&](uint32_t c) {
+        const uint32_t cs = c * C;
+        return (limit == 0u || last_pos < cs) ? 0u : (chunk_end(c) - cs) / kTile + 1u;
+    };
+    // A 16-position tile starts 16-aligned, so with P >= 16 (PAGE16) it lies in
+    // one page and the page id is wave-uniform: it is read through the scalar
+    // path and does not serialize behind the vector loads in flight.
     auto load_tile = [&](Tile& T, uint32_t c, uint32_t j) {
-        const uint32_t p = min(c * C + j * kTile + tok, chunk_end(c));
-        const uint32_t page = pt[p >> ly.log2p];
+        const uint32_t t0 = c * C + j * kTile;
+        const uint32_t p = min(t0 + tok, chunk_end(c));
+        uint32_t page;
+        if constexpr (PAGE16)
+            page = ((const __attribute__((address_space(4))) uint32_t*)(pt))
+                [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)];
+        else
+            page = pt[p >> ly.log2p];
         const uint16_t* src = pool + token_base(ly, layer, page, p & ly.pmask) + kvcol;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -159,7 +179,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             T.v[m] = ld16(src + 256u + 32u * m);
         }
     };
-    // Next (chunk, tile) of this wave after (c, j); returns false at the end.
+    // Next (chunk, tile) of this wave after (c, j); false past the range.
     auto advance = [&](uint32_t& c, uint32_t& j) {
         j += kWaves;
         while (c < c_end && j >= chunk_tiles(c)) {
@@ -169,16 +189,18 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         return c < c_end;
     };
 
-    Tile cur;
-    uint32_t lc = c_first, lj = wave;  // the tile held in `cur` once loaded
-    bool have = wave < chunk_tiles(c_first) || advance(lc, lj);
-    if (have) load_tile(cur, lc, lj);
-
     // Phase0 set-up: cos/sin of position `limit`; the block owning `limit`
     // builds the rotated K and the V of that token in LDS and stores both to
     // the pool. Lanes whose tile row is `limit` take these values from LDS
     // (their pool load of that slot may race with the store and is replaced).
-    const bool owner = PH0 && limit / C < c_end && limit < NC * C;
+    const bool owner = limit / C < c_end && limit < NC * C;
+    Tile A, B;
+    uint32_t ac = c_first, aj = wave;
+    bool a_ok = false;
+    if constexpr (TPW == 0) {
+        a_ok = wave < chunk_tiles(c_first) || advance(ac, aj);
+        if (a_ok) load_tile(A, ac, aj);
+    }
     if (PH0) {
         if (tid < 64u) {
             float c, sn;
@@ -203,6 +225,16 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             dst[tid] = lo;
             dst[tid + 64u] = hi;
             *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = v2;
+        }
+        __syncthreads();
+    } else {
+        if (owner && tid < 64u) {  // K|V of `limit` from the pool into LDS
+            const uint32_t page = pt[limit >> ly.log2p];
+            const uint16_t* src =
+                pool + token_base(ly, layer, page, limit & ly.pmask) + kvh * kD;
+            const uint32_t h = tid >> 5, d = (tid & 31u) * 4u;  // 32 lanes per half
+            *reinterpret_cast<uint2*>(&s_fresh[128u * h + d]) =
+                *reinterpret_cast<const uint2*>(src + 256u * h + d);
         }
         __syncthreads();
     }
@@ -246,84 +278,80 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     for (int i = 0; i < 4; ++i)
         ident[i] = (4u * grp + (uint32_t)i == tok) ? (short)0x3F80 : (short)0;
 
-    for (uint32_t c = c_first; c < c_end; ++c) {
-        const uint32_t cstart = c * C;
-        const uint32_t cend = chunk_end(c);
-        float m_run = -INFINITY, l_run = 0.f;
-        f32x4 acc[4][2];
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 acc[4][2];
+    auto reset_state = [&]() {
+        m_run = -INFINITY;
+        l_run = 0.f;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int h = 0; h < 2; ++h) acc[m][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    reset_state();
+    uint32_t cc = c_first;  // chunk whose state is accumulating
 
-        while (have && lc == c) {
-            const uint32_t j = lj;
-            uint32_t nc = lc, nj = lj;
-            const bool has_next = advance(nc, nj);
-            Tile nxt;
-            if (has_next) load_tile(nxt, nc, nj);
-            if (PH0 && owner && min(cstart + j * kTile + tok, cend) == limit) {
+    // Accumulates the tile starting at position `tstart` (rows after `tend`
+    // masked) into the current chunk state.
+    auto accumulate = [&](const Tile& T, uint32_t tstart, uint32_t tend) {
+        // S^T = K x Q^T
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    cur.k[m] = *reinterpret_cast<const uint4*>(&s_fresh[32u * m + 8u * grp]);
-                    cur.v[m] =
-                        *reinterpret_cast<const uint4*>(&s_fresh[128u + 32u * m + 8u * grp]);
-                }
-            }
-
-            // S^T = K x Q^T
-            f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < 4; ++m)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[m]), qb[m], s, 0, 0, 0);
+        const uint32_t pos0 = tstart + 4u * grp;
+        float sc[4];
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.k[m]), qb[m], s,
-                                                            0, 0, 0);
-            const uint32_t pos0 = cstart + j * kTile + 4u * grp;
-            float sc[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                float v;
-                {
+        for (int jj = 0; jj < 4; ++jj) {
+            float v;
+            {
 #pragma clang fp contract(off)
-                    v = s[jj] * kScoreScale;
-                }
-                sc[jj] = (pos0 + (uint32_t)jj <= cend) ? v : -INFINITY;
+                v = s[jj] * kScoreScale;
             }
-            float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-            tm = fmaxf(tm, __shfl_xor(tm, 16));
-            tm = fmaxf(tm, __shfl_xor(tm, 32));
-            const float mn = fmaxf(m_run, tm);
-            const float renew = (m_run == -INFINITY) ? 0.f : __expf(m_run - mn);
-            float p[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) p[jj] = __expf(sc[jj] - mn);
-            float ls = (p[0] + p[1]) + (p[2] + p[3]);
-            ls += __shfl_xor(ls, 16);
-            ls += __shfl_xor(ls, 32);
-            l_run = l_run * renew + ls;
-            m_run = mn;
-            s16x4 pb;
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) pb[jj] = (short)f32_to_bf16(p[jj]);
-
-#pragma unroll
-            for (int m = 0; m < 4; ++m)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                    const f32x4 vt = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                        half_s16x4(cur.v[m], h), ident, z, 0, 0, 0);
-                    acc[m][h] = acc[m][h] * renew;
-                    acc[m][h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                        trunc_bf16x4(vt), pb, acc[m][h], 0, 0, 0);
-                }
-            have = has_next;
-            lc = nc;
-            lj = nj;
-            if (has_next) cur = nxt;
+            sc[jj] = (pos0 + (uint32_t)jj <= tend) ? v : -INFINITY;
         }
-
-        // Fold the 4 wave states of chunk c (fixed wave order) through LDS.
-        const uint32_t b = c & 1u;
+        float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        tm = fmaxf(tm, __shfl_xor(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        const float mn = fmaxf(m_run, tm);
+        const float renew = (m_run == -INFINITY) ? 0.f : __expf(m_run - mn);
+        float p[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) p[jj] = __expf(sc[jj] - mn);
+        float ls = (p[0] + p[1]) + (p[2] + p[3]);
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        l_run = l_run * renew + ls;
+        m_run = mn;
+        s16x4 pb;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) pb[jj] = (short)f32_to_bf16(p[jj]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                const f32x4 vt = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                    half_s16x4(T.v[m], h), ident, z, 0, 0, 0);
+                acc[m][h] = acc[m][h] * renew;
+                acc[m][h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(trunc_bf16x4(vt), pb,
+                                                                      acc[m][h], 0, 0, 0);
+            }
+    };
+    // Folds the 4 wave states of chunk cc (fixed wave order) through LDS and
+    // writes its partial / output. Every wave calls it once per chunk, in
+    // chunk order (one barrier per chunk; LDS double-buffered by parity).
+    auto fold = [&]() {
+        if (owner && wave == 0u && cc == limit / C) {
+            Tile F;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                F.k[m] = *reinterpret_cast<const uint4*>(&s_fresh[32u * m + 8u * grp]);
+                F.v[m] = *reinterpret_cast<const uint4*>(&s_fresh[128u + 32u * m + 8u * grp]);
+            }
+            accumulate(F, limit, limit);
+        }
+        const uint32_t b = cc & 1u;
         if (tok < kGroup) {
             if (grp == 0u) {
                 s_m[b][wave][tok] = m_run;
@@ -344,33 +372,96 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         for (uint32_t w = 0; w < kWaves; ++w)
             if (s_l[b][w][head] != 0.f) M = fmaxf(M, s_m[b][w][head]);
         float L = 0.f;
-        f32x4 A = {0.f, 0.f, 0.f, 0.f};
+        f32x4 Acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t w = 0; w < kWaves; ++w) {
             const float lw = s_l[b][w][head];
             if (lw == 0.f) continue;
             const float f = __expf(s_m[b][w][head] - M);
             L += lw * f;
-            A += *reinterpret_cast<const f32x4*>(&s_acc[b][w][head][d4]) * f;
+            Acc += *reinterpret_cast<const f32x4*>(&s_acc[b][w][head][d4]) * f;
         }
         const uint32_t qh = kvh * kGroup + head;
         if (limit < C) {
             uint16_t o[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(L > 0.f ? A[i] / L : 0.f);
+            for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(L > 0.f ? Acc[i] / L : 0.f);
             *reinterpret_cast<uint2*>(a.out + qh * kD + d4) =
                 make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
                            (uint32_t)o[2] | ((uint32_t)o[3] << 16));
         } else {
-            float* pw = a.partials + ((size_t)qh * NC + c) * kPartial;
+            float* pw = a.partials + ((size_t)qh * NC + cc) * kPartial;
             if (d4 == 0u) {
                 pw[0] = M;
                 pw[1] = L;
             }
-            *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(A[0], A[1]);
-            *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(A[2], A[3]);
+            *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(Acc[0], Acc[1]);
+            *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(Acc[2], Acc[3]);
+        }
+        reset_state();
+        ++cc;
+    };
+
+    // Accumulates tile (c, j) held in T into the state of chunk c (folding any
+    // chunks before c first).
+    auto process = [&](const Tile& T, uint32_t c, uint32_t j) {
+        while (cc < c) fold();
+        accumulate(T, c * C + j * kTile, chunk_end(c));
+    };
+
+    if constexpr (TPW > 0) {
+        // Straight-line schedule (C == 64 * TPW): wave w owns tiles
+        // j = w + 4i, i < TPW, of every chunk. Chunks are walked in pairs with
+        // the tile loop fully unrolled, so the ring slot of every tile is a
+        // compile-time constant and the load of the next tile is always
+        // issued (clamped to an already-fetched tile past the range end)
+        // before the current one computes; the wait before each compute then
+        // covers only the older load group.
+        auto clamp_load = [&](Tile& T, uint32_t c, uint32_t i) {
+            const uint32_t cl = c < c_end ? c : c_end - 1u;
+            const uint32_t nt = chunk_tiles(cl);
+            uint32_t j = wave + 4u * i;
+            if (c >= c_end) j = wave + 4u * (TPW - 1u);
+            if (nt == 0u) j = 0u;
+            else if (j >= nt) j = nt - 1u;
+            load_tile(T, cl, j);
+        };
+        Tile R[2];
+        clamp_load(R[0], c_first, 0u);
+        for (uint32_t c = c_first; c < c_end; c += 2u) {
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) {
+                const uint32_t cc2 = c + h;
+#pragma unroll
+                for (uint32_t i = 0; i < TPW; ++i) {
+                    const uint32_t slot = (h * TPW + i) & 1u;
+                    if (i + 1u < TPW) clamp_load(R[slot ^ 1u], cc2, i + 1u);
+                    else clamp_load(R[slot ^ 1u], cc2 + 1u, 0u);
+                    const uint32_t j = wave + 4u * i;
+                    if (cc2 < c_end && j < chunk_tiles(cc2)) {
+                        while (cc < cc2) fold();
+                        accumulate(R[slot], cc2 * C + j * kTile, chunk_end(cc2));
+                    }
+                }
+            }
+        }
+    } else {
+        // Generic schedule (any C multiple of 16): ping-pong over two tiles.
+        while (a_ok) {
+            uint32_t bc = ac, bj = aj;
+            const bool b_ok = advance(bc, bj);
+            if (b_ok) load_tile(B, bc, bj);
+            process(A, ac, aj);
+            if (!b_ok) break;
+            uint32_t nc = bc, nj = bj;
+            a_ok = advance(nc, nj);
+            if (a_ok) load_tile(A, nc, nj);
+            process(B, bc, bj);
+            ac = nc;
+            aj = nj;
         }
     }
+    while (cc < c_end) fold();
 }
 
 #if MCKV_WAVES_PER_EU
@@ -381,7 +472,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 // grid = (ceil(NC / cpw), 2 kv heads, B slots). Single-session launches pass
 // B = 1 and the direct pointers; batched launches resolve per-slot pointers
 // from device tables.
-template <bool PH0, bool BATCH>
+template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW>
 __global__ void __launch_bounds__(kThreads) MCKV_CHUNK_ATTR decode_chunk_kernel(
     const uint16_t* __restrict__ q_rows, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t layer,
@@ -397,7 +488,8 @@ __global__ void __launch_bounds__(kThreads) MCKV_CHUNK_ATTR decode_chunk_kernel(
     a.pool = BATCH ? slot_kv[slot] : pool;
     a.partials = partials + (size_t)slot * kHq * NC * kPartial;
     a.out = out + (size_t)slot * kHq * kD;
-    decode_range_body<PH0>(a, layer, ly, NC, inv_freq, C, blockIdx.y, blockIdx.x * cpw, cpw);
+    decode_range_body<PH0, PAGE16, TPW>(a, layer, ly, NC, inv_freq, C, blockIdx.y,
+                                   blockIdx.x * cpw, cpw);
 }
 
 __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
@@ -536,14 +628,28 @@ mc_status_t launch_chunks(const uint16_t* q, const uint32_t* d_pos,
                           hipStream_t st, const float* inv_freq, uint32_t C) {
     const uint32_t cpw = chunks_per_block(NC, B, C);
     const dim3 grid((NC + cpw - 1u) / cpw, kHkv, B);
-    if (inv_freq != nullptr)
-        hipLaunchKernelGGL((decode_chunk_kernel<true, BATCH>), grid, dim3(kThreads), 0,
-                           st, q, d_pos, slot_pos, layer, pt, slot_pt, pool, slot_kv, ly,
-                           partials, NC, out, inv_freq, C, cpw);
-    else
-        hipLaunchKernelGGL((decode_chunk_kernel<false, BATCH>), grid, dim3(kThreads),
-                           0, st, q, d_pos, slot_pos, layer, pt, slot_pt, pool, slot_kv,
-                           ly, partials, NC, out, inv_freq, C, cpw);
+#define MCKV_LAUNCH_CHUNK(PH, PG, TP)                                                      \
+    hipLaunchKernelGGL((decode_chunk_kernel<PH, BATCH, PG, TP>), grid, dim3(kThreads), 0, st, \
+                       q, d_pos, slot_pos, layer, pt, slot_pt, pool, slot_kv, ly, partials,  \
+                       NC, out, inv_freq, C, cpw)
+#define MCKV_LAUNCH_TPW(PH, PG)                          \
+    switch (C) {                                         \
+        case 64: MCKV_LAUNCH_CHUNK(PH, PG, 1u); break;   \
+        case 128: MCKV_LAUNCH_CHUNK(PH, PG, 2u); break;  \
+        case 256: MCKV_LAUNCH_CHUNK(PH, PG, 4u); break;  \
+        case 512: MCKV_LAUNCH_CHUNK(PH, PG, 8u); break;  \
+        default: MCKV_LAUNCH_CHUNK(PH, PG, 0u); break;   \
+    }
+    const bool page16 = ly.log2p >= 4u;
+    if (inv_freq != nullptr) {
+        if (page16) MCKV_LAUNCH_TPW(true, true)
+        else MCKV_LAUNCH_TPW(true, false)
+    } else {
+        if (page16) MCKV_LAUNCH_TPW(false, true)
+        else MCKV_LAUNCH_TPW(false, false)
+    }
+#undef MCKV_LAUNCH_TPW
+#undef MCKV_LAUNCH_CHUNK
     return check_launch("decode attention chunk launch failed");
 }
 
