@@ -131,7 +131,7 @@ def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
     inv = torch.empty(64, dtype=torch.float32, device=dev)
     kvm.launch_rope_inv_freq_init(inv, 5e6)
     parts = torch.empty(16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.empty(16 * 32 * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
     out = torch.empty(LAYERS * 2048, dtype=torch.int16, device=dev)
     def step_on(pool):
         def f():
@@ -189,7 +189,7 @@ def bench_decode_batch(kvm, torch, dev, timer, B, ctx, steps, warmup):
     inv = torch.empty(64, dtype=torch.float32, device=dev)
     kvm.launch_rope_inv_freq_init(inv, 5e6)
     parts = torch.empty(B * 16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.empty(B * 16 * 32 * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(B * (16 * 32 * 130 + 2), dtype=torch.float32, device=dev)
     out = torch.empty(B * 2048, dtype=torch.int16, device=dev)
 
     def step_f():

@@ -135,7 +135,8 @@ mc_status_t mc_kv_rope_append(uint16_t* d_qkv, uint32_t tokens,
  * Attends positions 0..limit (limit = *d_pos) of one session. Chunk kernel
  * writes partials [16][max_chunks][130]; if limit < chunk_pos it writes
  * d_out [2048] directly. d_partials2 != NULL selects the two-level merge
- * (level-2 partials [16][32][130]); NULL selects the one-level merge.
+ * (level-2 partials [16][32][130]); NULL selects the one-level merge. With
+ * max_chunks <= 32 the two levels reduce exactly to one fold kernel.
  * d_inv_freq != NULL enables phase0: q and k of position `limit` are rotated
  * from d_q_rows, K/V of `limit` are written to the pool (pool may be written
  * only in that case). chunk_pos must be a multiple of 16. */

@@ -62,6 +62,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kWaves = 4;
 constexpr uint32_t kTile = 16;
+constexpr uint32_t kPageCache = 128;  // page ids staged in LDS per block
+#ifndef MCKV_FOLD_SLOTS
+#define MCKV_FOLD_SLOTS 2
+#endif
+constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 
 // Tuning knobs (compile-time): tiles in flight per wave beyond the one being
 // computed, forced waves per SIMD (0 = compiler choice), streaming loads.
@@ -69,7 +74,10 @@ constexpr uint32_t kTile = 16;
 #define MCKV_PREFETCH 1
 #endif
 #ifndef MCKV_WAVES_PER_EU
-#define MCKV_WAVES_PER_EU 0
+#define MCKV_WAVES_PER_EU 2
+#endif
+#ifndef MCKV_RING
+#define MCKV_RING 2
 #endif
 #ifndef MCKV_NT_LOADS
 #define MCKV_NT_LOADS 0
@@ -129,8 +137,9 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                                                   uint32_t c_first, uint32_t cpw) {
     __shared__ float s_cs[64], s_sn[64];
     __shared__ __align__(16) uint16_t s_fresh[256];  // phase0: K | V of `limit`
-    __shared__ float s_m[2][kWaves][kGroup], s_l[2][kWaves][kGroup];
-    __shared__ __align__(16) float s_acc[2][kWaves][kGroup][kD];
+    __shared__ uint32_t s_pages[kPageCache];         // page ids of this block's range
+    __shared__ float s_m[kFoldSlots][kWaves][kGroup], s_l[kFoldSlots][kWaves][kGroup];
+    __shared__ __align__(16) float s_acc[kFoldSlots][kWaves][kGroup][kD];
 
     const uint32_t limit = a.limit;
     const uint32_t nvalid = min(limit / C + 1u, NC);
@@ -163,11 +172,22 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // A 16-position tile starts 16-aligned, so with P >= 16 (PAGE16) it lies in
     // one page and the page id is wave-uniform: it is read through the scalar
     // path and does not serialize behind the vector loads in flight.
+    // Page ids of the block's position range, staged once into LDS (read by
+    // all tiles with a short LDS latency instead of a scalar-cache miss in
+    // front of every tile's loads).
+    const uint32_t page0 = (c_first * C) >> ly.log2p;
+    const uint32_t npages_rng = ((min(c_end * C, limit + 1u) - 1u) >> ly.log2p) - page0 + 1u;
+    const bool cached_pages = PAGE16 && npages_rng <= kPageCache;
+    if (cached_pages)
+        for (uint32_t i = tid; i < npages_rng; i += kThreads) s_pages[i] = pt[page0 + i];
+    __syncthreads();
     auto load_tile = [&](Tile& T, uint32_t c, uint32_t j) {
         const uint32_t t0 = c * C + j * kTile;
         const uint32_t p = min(t0 + tok, chunk_end(c));
         uint32_t page;
-        if constexpr (PAGE16)
+        if (PAGE16 && cached_pages)
+            page = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
+        else if constexpr (PAGE16)
             page = ((const __attribute__((address_space(4))) uint32_t*)(pt))
                 [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)];
         else
@@ -294,6 +314,15 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // Accumulates the tile starting at position `tstart` (rows after `tend`
     // masked) into the current chunk state.
     auto accumulate = [&](const Tile& T, uint32_t tstart, uint32_t tend) {
+#ifdef MCKV_PROBE_NO_COMPUTE
+        {
+            uint32_t x = 0;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) x ^= T.k[m].x ^ T.k[m].w ^ T.v[m].y ^ T.v[m].z;
+            l_run += (float)(x & 1u);
+            return;
+        }
+#endif
         // S^T = K x Q^T
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -338,9 +367,53 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                                                                       acc[m][h], 0, 0, 0);
             }
     };
-    // Folds the 4 wave states of chunk cc (fixed wave order) through LDS and
-    // writes its partial / output. Every wave calls it once per chunk, in
-    // chunk order (one barrier per chunk; LDS double-buffered by parity).
+    // Chunk completion. Each wave stashes its state of chunk cc into an LDS
+    // slot (no barrier); after kFoldSlots chunks, or at the end of the range,
+    // `flush` folds the stashed chunks across the 4 waves (fixed wave order)
+    // and writes their partials / output. Every wave stashes every chunk once,
+    // in chunk order, so the flush barriers line up across waves.
+    uint32_t nstash = 0;  // wave-uniform
+    auto flush = [&]() {
+        __syncthreads();
+        const uint32_t head = tid >> 5;        // 0..7
+        const uint32_t d4 = (tid & 31u) * 4u;  // 4 dims
+        const uint32_t qh = kvh * kGroup + head;
+        for (uint32_t k = 0; k < nstash; ++k) {
+            const uint32_t chunk = cc - nstash + k;
+            float M = -INFINITY;
+#pragma unroll
+            for (uint32_t w = 0; w < kWaves; ++w)
+                if (s_l[k][w][head] != 0.f) M = fmaxf(M, s_m[k][w][head]);
+            float L = 0.f;
+            f32x4 Acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (uint32_t w = 0; w < kWaves; ++w) {
+                const float lw = s_l[k][w][head];
+                if (lw == 0.f) continue;
+                const float f = __expf(s_m[k][w][head] - M);
+                L += lw * f;
+                Acc += *reinterpret_cast<const f32x4*>(&s_acc[k][w][head][d4]) * f;
+            }
+            if (limit < C) {
+                uint16_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(L > 0.f ? Acc[i] / L : 0.f);
+                *reinterpret_cast<uint2*>(a.out + qh * kD + d4) =
+                    make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
+                               (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+            } else {
+                float* pw = a.partials + ((size_t)qh * NC + chunk) * kPartial;
+                if (d4 == 0u) {
+                    pw[0] = M;
+                    pw[1] = L;
+                }
+                *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(Acc[0], Acc[1]);
+                *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(Acc[2], Acc[3]);
+            }
+        }
+        nstash = 0;
+        if (cc < c_end) __syncthreads();  // slots are reused by later chunks
+    };
     auto fold = [&]() {
         if (owner && wave == 0u && cc == limit / C) {
             Tile F;
@@ -351,59 +424,24 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             }
             accumulate(F, limit, limit);
         }
-        const uint32_t b = cc & 1u;
+        const uint32_t k = nstash;
         if (tok < kGroup) {
             if (grp == 0u) {
-                s_m[b][wave][tok] = m_run;
-                s_l[b][wave][tok] = l_run;
+                s_m[k][wave][tok] = m_run;
+                s_l[k][wave][tok] = l_run;
             }
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
                     *reinterpret_cast<f32x4*>(
-                        &s_acc[b][wave][tok][32u * m + 8u * grp + 4u * h]) = acc[m][h];
-        }
-        __syncthreads();
-        const uint32_t head = tid >> 5;        // 0..7
-        const uint32_t d4 = (tid & 31u) * 4u;  // 4 dims
-        float M = -INFINITY;
-#pragma unroll
-        for (uint32_t w = 0; w < kWaves; ++w)
-            if (s_l[b][w][head] != 0.f) M = fmaxf(M, s_m[b][w][head]);
-        float L = 0.f;
-        f32x4 Acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (uint32_t w = 0; w < kWaves; ++w) {
-            const float lw = s_l[b][w][head];
-            if (lw == 0.f) continue;
-            const float f = __expf(s_m[b][w][head] - M);
-            L += lw * f;
-            Acc += *reinterpret_cast<const f32x4*>(&s_acc[b][w][head][d4]) * f;
-        }
-        const uint32_t qh = kvh * kGroup + head;
-        if (limit < C) {
-            uint16_t o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(L > 0.f ? Acc[i] / L : 0.f);
-            *reinterpret_cast<uint2*>(a.out + qh * kD + d4) =
-                make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
-                           (uint32_t)o[2] | ((uint32_t)o[3] << 16));
-        } else {
-            float* pw = a.partials + ((size_t)qh * NC + cc) * kPartial;
-            if (d4 == 0u) {
-                pw[0] = M;
-                pw[1] = L;
-            }
-            *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(Acc[0], Acc[1]);
-            *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(Acc[2], Acc[3]);
+                        &s_acc[k][wave][tok][32u * m + 8u * grp + 4u * h]) = acc[m][h];
         }
         reset_state();
         ++cc;
+        if (++nstash == kFoldSlots) flush();
     };
 
-    // Accumulates tile (c, j) held in T into the state of chunk c (folding any
-    // chunks before c first).
     auto process = [&](const Tile& T, uint32_t c, uint32_t j) {
         while (cc < c) fold();
         accumulate(T, c * C + j * kTile, chunk_end(c));
@@ -426,21 +464,28 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             else if (j >= nt) j = nt - 1u;
             load_tile(T, cl, j);
         };
-        Tile R[2];
-        clamp_load(R[0], c_first, 0u);
-        for (uint32_t c = c_first; c < c_end; c += 2u) {
+        // Ring of MCKV_RING register tiles, MCKV_RING - 1 loads ahead; U
+        // chunks are unrolled per loop trip so that U * TPW is a multiple of
+        // the ring size and every slot index is a compile-time constant.
+        constexpr uint32_t RING = MCKV_RING;
+        constexpr uint32_t U = (TPW % RING == 0u) ? 1u : RING / (RING == 4u && TPW % 2u == 0u ? 2u : 1u);
+        static_assert((U * TPW) % RING == 0u, "ring slots must repeat per loop trip");
+        Tile R[RING];
 #pragma unroll
-            for (uint32_t h = 0; h < 2u; ++h) {
+        for (uint32_t g = 0; g + 1u < RING; ++g) clamp_load(R[g], c_first + g / TPW, g % TPW);
+        for (uint32_t c = c_first; c < c_end; c += U) {
+#pragma clang loop unroll(full)
+            for (uint32_t h = 0; h < U; ++h) {
                 const uint32_t cc2 = c + h;
-#pragma unroll
+#pragma clang loop unroll(full)
                 for (uint32_t i = 0; i < TPW; ++i) {
-                    const uint32_t slot = (h * TPW + i) & 1u;
-                    if (i + 1u < TPW) clamp_load(R[slot ^ 1u], cc2, i + 1u);
-                    else clamp_load(R[slot ^ 1u], cc2 + 1u, 0u);
+                    const uint32_t g = h * TPW + i;
+                    const uint32_t ga = g + RING - 1u;  // tile to prefetch
+                    clamp_load(R[ga % RING], c + ga / TPW, ga % TPW);
                     const uint32_t j = wave + 4u * i;
                     if (cc2 < c_end && j < chunk_tiles(cc2)) {
                         while (cc < cc2) fold();
-                        accumulate(R[slot], cc2 * C + j * kTile, chunk_end(cc2));
+                        accumulate(R[g % RING], cc2 * C + j * kTile, chunk_end(cc2));
                     }
                 }
             }
@@ -462,6 +507,8 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         }
     }
     while (cc < c_end) fold();
+    if (nstash != 0u) flush();
+
 }
 
 #if MCKV_WAVES_PER_EU
@@ -657,7 +704,10 @@ template <bool BATCH>
 mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
                          const uint32_t* const* slot_pos, uint32_t B, uint32_t NC,
                          uint32_t C, float* partials2, uint16_t* out, hipStream_t st) {
-    if (partials2 != nullptr) {
+    // With at most 32 chunks every level-2 split holds one chunk, merge_a would
+    // copy it exactly (m, l * 1, acc * 1), and merge_b's ascending fold equals
+    // the one-level fold: a single kernel gives the identical result.
+    if (partials2 != nullptr && NC > kSplit2) {
         hipLaunchKernelGGL((merge_a_kernel<BATCH>), dim3(B * kHq, kSplit2), dim3(128), 0,
                            st, partials, d_pos, slot_pos, NC, C, partials2);
         hipLaunchKernelGGL((merge_b_kernel<BATCH>), dim3(B * kHq), dim3(128), 0, st,
@@ -704,9 +754,19 @@ extern "C" mc_status_t mc_kv_attention_decode(
     const uint32_t* d_page_table, uint16_t* d_kv_pool, mc_kv_layout_t layout,
     float* d_partials, uint32_t max_chunks, uint16_t* d_out, void* stream,
     const float* d_inv_freq, uint32_t chunk_pos, float* d_partials2) {
-    const mc_status_t st = mc_kv_attention_decode_chunks(
-        d_q_rows, d_pos, layer, d_page_table, d_kv_pool, layout, d_partials,
-        max_chunks, d_out, stream, d_inv_freq, chunk_pos);
+    DevLayout ly;
+    if (d_q_rows == nullptr || d_pos == nullptr || d_page_table == nullptr ||
+        d_kv_pool == nullptr || d_partials == nullptr || d_out == nullptr ||
+        !layout_valid(layout, &ly) || layer >= layout.num_layers ||
+        !chunk_args_ok(max_chunks, chunk_pos)) {
+        set_error("mc_kv_attention_decode: invalid args (layer=%u max_chunks=%u "
+                  "chunk_pos=%u)",
+                  layer, max_chunks, chunk_pos);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    const mc_status_t st = launch_chunks<false>(
+        d_q_rows, d_pos, nullptr, 1, layer, d_page_table, nullptr, d_kv_pool, nullptr, ly,
+        d_partials, max_chunks, d_out, (hipStream_t)stream, d_inv_freq, chunk_pos);
     if (st != MC_OK) return st;
     return launch_merge<false>(d_partials, d_pos, nullptr, 1, max_chunks, chunk_pos,
                                d_partials2, d_out, (hipStream_t)stream);

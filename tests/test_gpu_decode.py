@@ -41,7 +41,7 @@ def run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, limit, C, NC, two_level
     d_pt = to_dev(np.asarray(pt, dtype=np.uint32), dev)
     d_pos = to_dev(np.array([limit], dtype=np.uint32), dev)
     parts = torch.full((16 * NC * 130,), float("nan"), dtype=torch.float32, device=dev)
-    parts2 = torch.full((16 * 32 * 130,), float("nan"), dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
     out = torch.zeros(2048, dtype=torch.int16, device=dev)
     kvm.launch_attention_decode(d_q, d_pos, layer, d_pt, d_pool, lay, parts, NC, out,
                                 d_inv_freq=inv, chunk_pos=C,
@@ -201,7 +201,7 @@ def test_phase0_matches_rope_then_attend(kvm, orc, dev, limit):
     d_pos = to_dev(np.array([limit], dtype=np.uint32), dev)
     kvm.launch_rope_kv(d_qkv_a, 1, d_pos, layer, d_pt, d_pool_a, lay, 5e6, d_inv_freq=inv)
     pa = torch.empty(16 * NC * 130, dtype=torch.float32, device=dev)
-    p2 = torch.empty(16 * 32 * 130, dtype=torch.float32, device=dev)
+    p2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
     out_a = torch.zeros(2048, dtype=torch.int16, device=dev)
     kvm.launch_attention_decode(d_qkv_a, d_pos, layer, d_pt, d_pool_a, lay, pa, NC, out_a,
                                 chunk_pos=64, d_partials2=p2)
@@ -252,7 +252,7 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed):
     tab = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64,
                                   device=dev)
     parts = torch.zeros(B * 16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.zeros(B * 16 * 32 * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(B * (16 * 32 * 130 + 2), dtype=torch.float32, device=dev)
     out = torch.zeros(B * 2048, dtype=torch.int16, device=dev)
     kvm.launch_attention_decode_batch(d_q, tab(d_lims), B, layer, tab(d_pts),
                                       tab([d_pool] * B), lay, parts, NC, out, d_inv_freq=inv,
@@ -268,7 +268,8 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed):
         o1 = torch.zeros(2048, dtype=torch.int16, device=dev)
         kvm.launch_attention_decode(to_dev(q[s], dev), d_lims[s], layer, d_pts[s], d_pool1,
                                     lay, p1, NC, o1, d_inv_freq=inv, chunk_pos=C,
-                                    d_partials2=parts2[:16 * 32 * 130].clone())
+                                    d_partials2=torch.zeros(16 * 32 * 130 + 2,
+                                                            dtype=torch.float32, device=dev))
         torch.cuda.synchronize()
         singles.append(from_dev(o1))
     assert np.array_equal(got, np.stack(singles)), "batched != single (bitwise)"
@@ -328,3 +329,53 @@ def test_decode_long_multichunk_blocks(kvm, orc, dev, ctx, C, ph0):
         assert np.array_equal(pool_after, pool_o)
     ref = orc.attn_ref(qkv_o, 1, limit, layer, pool_o, pt, P, maxp)[0]
     check_vs_ref(orc, got, ref, f"long ctx={ctx} C={C}")
+
+
+@pytest.mark.parametrize("ctx,C", [(2048, 64), (3000, 64), (40000, 128)])
+def test_repeat_launch_and_graph_replay(kvm, orc, dev, ctx, C):
+    """Repeated eager launches on the same scratch buffers give identical
+    outputs, and a captured HIP graph replayed several times (the limit
+    advanced by an eager device op between replays) matches eager launches
+    every time."""
+    import torch
+    rng = np.random.default_rng(ctx)
+    P, L, layer = 64, 1, 0
+    maxp = -(-(ctx + 8) // P)
+    pt = rng.permutation(maxp).astype(np.uint32)
+    lay = kvm.KvLayout(maxp, P, L)
+    pool = randn_bf16(rng, lay.total_elems(), 0.4)
+    q = randn_bf16(rng, 2560, 1.0)
+    NC = -(-(ctx + 8) // C)
+    d_pool, d_q, d_pt = to_dev(pool, dev), to_dev(q, dev), to_dev(pt, dev)
+    parts = torch.zeros(16 * NC * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
+    d_pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+
+    def run(out):
+        kvm.launch_attention_decode(d_q, d_pos, layer, d_pt, d_pool, lay, parts, NC, out,
+                                    chunk_pos=C, d_partials2=parts2)
+    eager = []
+    for _ in range(3):
+        o = torch.zeros(2048, dtype=torch.int16, device=dev)
+        run(o)
+        torch.cuda.synchronize()
+        eager.append(from_dev(o))
+    assert all(np.array_equal(eager[0], e) for e in eager[1:])
+    ref = orc.attn_ref(q.reshape(1, 2560), 1, ctx - 1, layer, pool, pt, P, maxp)[0]
+    check_vs_ref(orc, eager[0], ref, f"fused ctx={ctx}")
+    # graph capture of one launch; replays at limits ctx-1, ctx, ..., ctx+3
+    gout = torch.zeros(2048, dtype=torch.int16, device=dev)
+    run(gout)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(gout)
+    for k in range(4):
+        d_pos.fill_(ctx - 1 + k)
+        g.replay()
+        torch.cuda.synchronize()
+        got = from_dev(gout)
+        e = torch.zeros(2048, dtype=torch.int16, device=dev)
+        run(e)
+        torch.cuda.synchronize()
+        assert np.array_equal(got, from_dev(e)), f"replay {k}"
