@@ -347,9 +347,13 @@ def main():
     }
     if head:
         ach = head["chunk_kernel_gbs"]
+        traffic = None  # HBM bytes per launch measured with rocprofv3 PMC passes
+        tf = os.path.join(ROOT, "profiles", "decode_chunk_c4_traffic.txt")
+        if os.path.exists(tf):
+            traffic = json.load(open(tf)).get("traffic_bytes")
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                            "traffic": None,
+                            "traffic": traffic,
                             "kernel": "decode_chunk_kernel<true,false> (C4 layer)",
                             "kernel_us": round(head["chunk_kernel_us"], 3)}
     print(json.dumps(line), flush=True)
