@@ -178,14 +178,14 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     const uint32_t page0 = (c_first * C) >> ly.log2p;
     const uint32_t npages_rng = ((min(c_end * C, limit + 1u) - 1u) >> ly.log2p) - page0 + 1u;
     const bool cached_pages = PAGE16 && npages_rng <= kPageCache;
-    if (cached_pages)
-        for (uint32_t i = tid; i < npages_rng; i += kThreads) s_pages[i] = pt[page0 + i];
-    __syncthreads();
-    auto load_tile = [&](Tile& T, uint32_t c, uint32_t j) {
+    // `direct` reads the page id from the table itself (scalar path for
+    // PAGE16) instead of the LDS copy; the first tiles use it so that they
+    // do not wait for the staging barrier.
+    auto load_tile = [&](Tile& T, uint32_t c, uint32_t j, bool direct) {
         const uint32_t t0 = c * C + j * kTile;
         const uint32_t p = min(t0 + tok, chunk_end(c));
         uint32_t page;
-        if (PAGE16 && cached_pages)
+        if (PAGE16 && cached_pages && !direct)
             page = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
         else if constexpr (PAGE16)
             page = ((const __attribute__((address_space(4))) uint32_t*)(pt))
@@ -208,68 +208,104 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         }
         return c < c_end;
     };
+    // Straight-line schedule helper: tile i (0..TPW-1) of this wave in chunk
+    // c, clamped to an existing tile past the end of the range (the clamped
+    // load re-reads a tile and is never accumulated).
+    auto clamp_load = [&](Tile& T, uint32_t c, uint32_t i, bool direct) {
+        const uint32_t cl = c < c_end ? c : c_end - 1u;
+        const uint32_t nt = chunk_tiles(cl);
+        uint32_t j = wave + 4u * i;
+        if (c >= c_end) j = wave + 4u * (TPW - 1u);
+        if (nt == 0u) j = 0u;
+        else if (j >= nt) j = nt - 1u;
+        load_tile(T, cl, j, direct);
+    };
 
-    // Phase0 set-up: cos/sin of position `limit`; the block owning `limit`
-    // builds the rotated K and the V of that token in LDS and stores both to
-    // the pool. Lanes whose tile row is `limit` take these values from LDS
-    // (their pool load of that slot may race with the store and is replaced).
+    // Start-up, ordered for latency: (a) loads that need nothing computed
+    // (q, inv_freq, the new token's k/v), (b) the block's page ids, (c) the
+    // first K/V tiles (one dependent scalar load after `limit`), and only
+    // then (d) the work that waits for (a) and (b). Phase0: cos/sin of
+    // position `limit`; the block owning `limit` builds the rotated K and the
+    // V of that token in LDS and stores both to the pool.
     const bool owner = limit / C < c_end && limit < NC * C;
-    Tile A, B;
+    const bool real = tok < kGroup;
+    // All start-up loads are unconditional (addresses clamped) so that no
+    // divergent branch makes the compiler wait for them before the first
+    // K/V tiles are issued.
+    uint4 qr[4];
+    {
+        const uint16_t* qsrc = q_row + (kvh * kGroup + (real ? tok : 0u)) * kD + 8u * grp;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) qr[m] = *reinterpret_cast<const uint4*>(qsrc + 32u * m);
+    }
+    const uint32_t t64 = tid & 63u;
+    float invf = 0.f;
+    uint16_t kx = 0, kx2 = 0;
+    uint32_t fresh_v = 0u;
+    uint2 fresh_kv = make_uint2(0u, 0u);
+    const uint32_t limit_page =
+        owner ? ((const __attribute__((address_space(4))) uint32_t*)(pt))[limit >> ly.log2p]
+              : 0u;
+    if (PH0) {  // every block reads the new token's k/v (a few cached bytes)
+        invf = inv_freq[t64];
+        const uint16_t* kr = q_row + kKCol + kvh * kD;
+        kx = kr[t64];
+        kx2 = kr[t64 + 64u];
+        fresh_v = *reinterpret_cast<const uint32_t*>(q_row + kVCol + kvh * kD + 2u * t64);
+    } else if (owner) {  // K|V of `limit` from the pool, 32 lanes per half
+        const uint16_t* src =
+            pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
+        fresh_kv = *reinterpret_cast<const uint2*>(src + 256u * (t64 >> 5) + (t64 & 31u) * 4u);
+    }
+    uint32_t staged_page = 0u;
+    if (cached_pages) staged_page = pt[page0 + min(tid, npages_rng - 1u)];
+
+    constexpr uint32_t RING = MCKV_RING;
+    Tile R[RING];
+    Tile& A = R[0];
+    Tile& B = R[RING > 1u ? 1u : 0u];
     uint32_t ac = c_first, aj = wave;
     bool a_ok = false;
-    if constexpr (TPW == 0) {
+    if constexpr (TPW > 0) {
+#pragma unroll
+        for (uint32_t g = 0; g + 1u < RING; ++g)
+            clamp_load(R[g], c_first + g / TPW, g % TPW, true);
+    } else {
         a_ok = wave < chunk_tiles(c_first) || advance(ac, aj);
-        if (a_ok) load_tile(A, ac, aj);
+        if (a_ok) load_tile(A, ac, aj, true);
     }
-    if (PH0) {
-        if (tid < 64u) {
+
+    if (cached_pages && tid < npages_rng) s_pages[tid] = staged_page;
+    if (tid < 64u) {
+        if (PH0) {
             float c, sn;
-            rope_sincos((float)limit * inv_freq[tid], &c, &sn);
+            rope_sincos((float)limit * invf, &c, &sn);
             s_cs[tid] = c;
             s_sn[tid] = sn;
+            if (owner) {  // pair tid rotates dims tid and tid + 64
+                const float x = bf16_to_f32(kx), x2 = bf16_to_f32(kx2);
+                const uint16_t lo = f32_to_bf16(rope_rotate(x, x2, c, sn, true));
+                const uint16_t hi = f32_to_bf16(rope_rotate(x2, x, c, sn, false));
+                s_fresh[tid] = lo;
+                s_fresh[tid + 64u] = hi;
+                *reinterpret_cast<uint32_t*>(&s_fresh[128u + 2u * tid]) = fresh_v;
+                uint16_t* dst =
+                    pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
+                dst[tid] = lo;
+                dst[tid + 64u] = hi;
+                *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = fresh_v;
+            }
+        } else if (owner) {
+            const uint32_t h = tid >> 5, d = (tid & 31u) * 4u;
+            *reinterpret_cast<uint2*>(&s_fresh[128u * h + d]) = fresh_kv;
         }
-        __syncthreads();
-        if (owner && tid < 64u) {
-            const uint16_t* kr = q_row + kKCol + kvh * kD;
-            const uint16_t* vr = q_row + kVCol + kvh * kD;
-            const float x = bf16_to_f32(kr[tid]), x2 = bf16_to_f32(kr[tid + 64u]);
-            const uint16_t lo = f32_to_bf16(rope_rotate(x, x2, s_cs[tid], s_sn[tid], true));
-            const uint16_t hi =
-                f32_to_bf16(rope_rotate(x2, x, s_cs[tid], s_sn[tid], false));
-            const uint32_t v2 = *reinterpret_cast<const uint32_t*>(vr + 2u * tid);
-            s_fresh[tid] = lo;
-            s_fresh[tid + 64u] = hi;
-            *reinterpret_cast<uint32_t*>(&s_fresh[128u + 2u * tid]) = v2;
-            const uint32_t page = pt[limit >> ly.log2p];
-            uint16_t* dst = pool + token_base(ly, layer, page, limit & ly.pmask) + kvh * kD;
-            dst[tid] = lo;
-            dst[tid + 64u] = hi;
-            *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = v2;
-        }
-        __syncthreads();
-    } else {
-        if (owner && tid < 64u) {  // K|V of `limit` from the pool into LDS
-            const uint32_t page = pt[limit >> ly.log2p];
-            const uint16_t* src =
-                pool + token_base(ly, layer, page, limit & ly.pmask) + kvh * kD;
-            const uint32_t h = tid >> 5, d = (tid & 31u) * 4u;  // 32 lanes per half
-            *reinterpret_cast<uint2*>(&s_fresh[128u * h + d]) =
-                *reinterpret_cast<const uint2*>(src + 256u * h + d);
-        }
-        __syncthreads();
     }
+    __syncthreads();
 
     // Q^T B operand: lane holds q[head = tok][32m + 8*grp + i]; heads >= 8 zero.
     // Phase0 rotates q in registers (partner dim d^64 sits in block m^2).
     bf16x8 qb[4];
     {
-        uint4 qr[4];
-        const bool real = tok < kGroup;
-        const uint16_t* qsrc = q_row + (kvh * kGroup + (real ? tok : 0u)) * kD + 8u * grp;
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-            qr[m] = real ? *reinterpret_cast<const uint4*>(qsrc + 32u * m)
-                         : make_uint4(0u, 0u, 0u, 0u);
         if (PH0 && real) {
             uint4 rq[4];
 #pragma unroll
@@ -289,7 +325,8 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             for (int m = 0; m < 4; ++m) qr[m] = rq[m];
         }
 #pragma unroll
-        for (int m = 0; m < 4; ++m) qb[m] = as_bf16x8(qr[m]);
+        for (int m = 0; m < 4; ++m)
+            qb[m] = as_bf16x8(real ? qr[m] : make_uint4(0u, 0u, 0u, 0u));
     }
 
     // Identity B operand for the transpose: B[k][c] = (k == c), k = 4*grp + i.
@@ -455,24 +492,11 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         // issued (clamped to an already-fetched tile past the range end)
         // before the current one computes; the wait before each compute then
         // covers only the older load group.
-        auto clamp_load = [&](Tile& T, uint32_t c, uint32_t i) {
-            const uint32_t cl = c < c_end ? c : c_end - 1u;
-            const uint32_t nt = chunk_tiles(cl);
-            uint32_t j = wave + 4u * i;
-            if (c >= c_end) j = wave + 4u * (TPW - 1u);
-            if (nt == 0u) j = 0u;
-            else if (j >= nt) j = nt - 1u;
-            load_tile(T, cl, j);
-        };
         // Ring of MCKV_RING register tiles, MCKV_RING - 1 loads ahead; U
         // chunks are unrolled per loop trip so that U * TPW is a multiple of
         // the ring size and every slot index is a compile-time constant.
-        constexpr uint32_t RING = MCKV_RING;
         constexpr uint32_t U = (TPW % RING == 0u) ? 1u : RING / (RING == 4u && TPW % 2u == 0u ? 2u : 1u);
         static_assert((U * TPW) % RING == 0u, "ring slots must repeat per loop trip");
-        Tile R[RING];
-#pragma unroll
-        for (uint32_t g = 0; g + 1u < RING; ++g) clamp_load(R[g], c_first + g / TPW, g % TPW);
         for (uint32_t c = c_first; c < c_end; c += U) {
 #pragma clang loop unroll(full)
             for (uint32_t h = 0; h < U; ++h) {
@@ -481,7 +505,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                 for (uint32_t i = 0; i < TPW; ++i) {
                     const uint32_t g = h * TPW + i;
                     const uint32_t ga = g + RING - 1u;  // tile to prefetch
-                    clamp_load(R[ga % RING], c + ga / TPW, ga % TPW);
+                    clamp_load(R[ga % RING], c + ga / TPW, ga % TPW, false);
                     const uint32_t j = wave + 4u * i;
                     if (cc2 < c_end && j < chunk_tiles(cc2)) {
                         while (cc < cc2) fold();
@@ -495,12 +519,12 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         while (a_ok) {
             uint32_t bc = ac, bj = aj;
             const bool b_ok = advance(bc, bj);
-            if (b_ok) load_tile(B, bc, bj);
+            if (b_ok) load_tile(B, bc, bj, false);
             process(A, ac, aj);
             if (!b_ok) break;
             uint32_t nc = bc, nj = bj;
             a_ok = advance(nc, nj);
-            if (a_ok) load_tile(A, nc, nj);
+            if (a_ok) load_tile(A, nc, nj, false);
             process(B, bc, bj);
             ac = nc;
             aj = nj;
@@ -591,8 +615,54 @@ __device__ __forceinline__ float fold_partials(const float* __restrict__ base,
     return A;
 }
 
+// Fold of at most NMAX <= 128 partials in ONE memory round: every thread
+// issues its NMAX acc loads and (thread i < n) the (m, l) of partial i before
+// anything waits, then M, the factors f_i and the ascending sums follow from
+// LDS and registers. Same arithmetic and order as fold_partials, so results
+// are bit-identical to it. Block = 128 threads, thread = dim.
+template <uint32_t NMAX>
+__device__ __forceinline__ float fold_partials_small(const float* __restrict__ base,
+                                                     size_t stride, uint32_t n,
+                                                     float& M_out, float& L_out) {
+    static_assert(NMAX <= 128u, "one (m, l) pair per thread");
+    __shared__ float s_f[NMAX], s_l[NMAX], s_red[2];
+    const uint32_t d = threadIdx.x;
+    float v[NMAX];
+#pragma unroll
+    for (uint32_t i = 0; i < NMAX; ++i) v[i] = (i < n) ? base[i * stride + 2u + d] : 0.f;
+    float m = -INFINITY, l = 0.f;
+    if (d < n) {
+        const float2 ml = *reinterpret_cast<const float2*>(base + d * stride);
+        m = ml.x;
+        l = ml.y;
+    }
+    float mx = (l != 0.f) ? m : -INFINITY;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((d & 63u) == 0u) s_red[d >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(s_red[0], s_red[1]);
+    if (d < NMAX) {
+        s_f[d] = (l != 0.f) ? expf(m - M) : 0.f;
+        s_l[d] = l;
+    }
+    __syncthreads();
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < NMAX; ++i) {
+        const float f = s_f[i];
+        const bool live = s_l[i] != 0.f;
+        L += live ? s_l[i] * f : 0.f;
+        A += live ? v[i] * f : 0.f;
+    }
+    M_out = M;
+    L_out = L;
+    return A;
+}
+
 // Level-1 -> level-2 merge. grid = (B*16, 32), block = 128 (thread = dim).
-template <bool BATCH>
+// NMAX >= ceil(NC / 32) selects the one-round fold; 0 the generic one.
+template <bool BATCH, uint32_t NMAX>
 __global__ void __launch_bounds__(128) merge_a_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
@@ -611,9 +681,12 @@ __global__ void __launch_bounds__(128) merge_a_kernel(
         return;
     }
     const float* P = partials + (((size_t)slot * kHq + qh) * NC + s) * kPartial;
-    float M, L;
-    const float A = fold_partials(P, (size_t)kSplit2 * kPartial, (nv - s + kSplit2 - 1u) / kSplit2,
-                                  M, L);
+    const uint32_t n = (nv - s + kSplit2 - 1u) / kSplit2;
+    float M, L, A;
+    if constexpr (NMAX > 0u)
+        A = fold_partials_small<NMAX>(P, (size_t)kSplit2 * kPartial, n, M, L);
+    else
+        A = fold_partials(P, (size_t)kSplit2 * kPartial, n, M, L);
     if (d == 0u) {
         pw2[0] = M;
         pw2[1] = L;
@@ -631,14 +704,14 @@ __global__ void __launch_bounds__(128) merge_b_kernel(
     const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
     if (n_valid_chunks(limit, C, NC) == 1u) return;
     float M, L;
-    const float A = fold_partials(partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial,
-                                  kPartial, kSplit2, M, L);
+    const float A = fold_partials_small<kSplit2>(
+        partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial, kPartial, kSplit2, M, L);
     out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
 }
 
 // One-level merge of all valid level-1 partials (used when no level-2 buffer
-// is given). grid = B*16, block = 128; the fold runs in pieces of kMaxFold.
-template <bool BATCH>
+// is given, or when NC <= 32). grid = B*16, block = 128; NMAX as in merge_a.
+template <bool BATCH, uint32_t NMAX>
 __global__ void __launch_bounds__(128) merge_p_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
@@ -647,9 +720,12 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
     const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
     const uint32_t nv = n_valid_chunks(limit, C, NC);
     if (nv == 1u) return;
-    float M, L;
-    const float A = fold_partials(partials + ((size_t)slot * kHq + qh) * NC * kPartial,
-                                  kPartial, nv, M, L);
+    const float* base = partials + ((size_t)slot * kHq + qh) * NC * kPartial;
+    float M, L, A;
+    if constexpr (NMAX > 0u)
+        A = fold_partials_small<NMAX>(base, kPartial, nv, M, L);
+    else
+        A = fold_partials(base, kPartial, nv, M, L);
     out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
 }
 
@@ -708,12 +784,23 @@ mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
     // copy it exactly (m, l * 1, acc * 1), and merge_b's ascending fold equals
     // the one-level fold: a single kernel gives the identical result.
     if (partials2 != nullptr && NC > kSplit2) {
-        hipLaunchKernelGGL((merge_a_kernel<BATCH>), dim3(B * kHq, kSplit2), dim3(128), 0,
-                           st, partials, d_pos, slot_pos, NC, C, partials2);
+        const dim3 ga(B * kHq, kSplit2);
+        if (NC <= 16u * kSplit2)
+            hipLaunchKernelGGL((merge_a_kernel<BATCH, 16u>), ga, dim3(128), 0, st, partials,
+                               d_pos, slot_pos, NC, C, partials2);
+        else if (NC <= 64u * kSplit2)
+            hipLaunchKernelGGL((merge_a_kernel<BATCH, 64u>), ga, dim3(128), 0, st, partials,
+                               d_pos, slot_pos, NC, C, partials2);
+        else
+            hipLaunchKernelGGL((merge_a_kernel<BATCH, 0u>), ga, dim3(128), 0, st, partials,
+                               d_pos, slot_pos, NC, C, partials2);
         hipLaunchKernelGGL((merge_b_kernel<BATCH>), dim3(B * kHq), dim3(128), 0, st,
                            partials2, d_pos, slot_pos, NC, C, out);
+    } else if (NC <= kSplit2) {
+        hipLaunchKernelGGL((merge_p_kernel<BATCH, kSplit2>), dim3(B * kHq), dim3(128), 0, st,
+                           partials, d_pos, slot_pos, NC, C, out);
     } else {
-        hipLaunchKernelGGL((merge_p_kernel<BATCH>), dim3(B * kHq), dim3(128), 0, st,
+        hipLaunchKernelGGL((merge_p_kernel<BATCH, 0u>), dim3(B * kHq), dim3(128), 0, st,
                            partials, d_pos, slot_pos, NC, C, out);
     }
     return check_launch("decode attention merge launch failed");
