@@ -569,7 +569,7 @@ __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
     return n > NC ? NC : n;
 }
 
-constexpr uint32_t kMaxFold = 2048;  // partials folded by one 128-thread block
+constexpr uint32_t kMaxFold = 2048;
 
 // Folds n partials {m, l, acc[128]} at base + i*stride (i ascending) with the
 // reference merge rule: M = max m over l != 0; f_i = exp(m_i - M);
@@ -615,27 +615,39 @@ __device__ __forceinline__ float fold_partials(const float* __restrict__ base,
     return A;
 }
 
-// Fold of at most NMAX <= 128 partials in ONE memory round: every thread
-// issues its NMAX acc loads and (thread i < n) the (m, l) of partial i before
-// anything waits, then M, the factors f_i and the ascending sums follow from
-// LDS and registers. Same arithmetic and order as fold_partials, so results
-// are bit-identical to it. Block = 128 threads, thread = dim.
+// Folds of at most NMAX <= 128 partials in ONE memory round, split in two
+// steps so that the loads can be issued before the decode limit is known:
+// load_partials reads `nload` partials (everything the buffer holds for this
+// fold; never more than it holds), fold_loaded then keeps the first n of
+// them. Same arithmetic and order as fold_partials (bit-identical results).
+// Block = 128 threads, thread = dim.
 template <uint32_t NMAX>
-__device__ __forceinline__ float fold_partials_small(const float* __restrict__ base,
-                                                     size_t stride, uint32_t n,
-                                                     float& M_out, float& L_out) {
+struct Loaded {
+    float v[NMAX];  // acc[d] of partial i
+    float m, l;     // (m, l) of partial threadIdx.x
+};
+
+template <uint32_t NMAX>
+__device__ __forceinline__ void load_partials(const float* __restrict__ base, size_t stride,
+                                              uint32_t nload, Loaded<NMAX>& x) {
     static_assert(NMAX <= 128u, "one (m, l) pair per thread");
+    const uint32_t d = threadIdx.x;
+#pragma unroll
+    for (uint32_t i = 0; i < NMAX; ++i)  // past nload: a repeated (never kept) load
+        x.v[i] = base[(i < nload ? i : nload - 1u) * stride + 2u + d];
+    const uint32_t di = d < nload ? d : nload - 1u;
+    const float2 ml = *reinterpret_cast<const float2*>(base + di * stride);
+    x.m = ml.x;
+    x.l = ml.y;
+}
+
+template <uint32_t NMAX>
+__device__ __forceinline__ float fold_loaded(const Loaded<NMAX>& x, uint32_t n, float& M_out,
+                                             float& L_out) {
     __shared__ float s_f[NMAX], s_l[NMAX], s_red[2];
     const uint32_t d = threadIdx.x;
-    float v[NMAX];
-#pragma unroll
-    for (uint32_t i = 0; i < NMAX; ++i) v[i] = (i < n) ? base[i * stride + 2u + d] : 0.f;
-    float m = -INFINITY, l = 0.f;
-    if (d < n) {
-        const float2 ml = *reinterpret_cast<const float2*>(base + d * stride);
-        m = ml.x;
-        l = ml.y;
-    }
+    const float m = x.m;
+    const float l = d < n ? x.l : 0.f;
     float mx = (l != 0.f) ? m : -INFINITY;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -653,7 +665,7 @@ __device__ __forceinline__ float fold_partials_small(const float* __restrict__ b
         const float f = s_f[i];
         const bool live = s_l[i] != 0.f;
         L += live ? s_l[i] * f : 0.f;
-        A += live ? v[i] * f : 0.f;
+        A += live ? x.v[i] * f : 0.f;
     }
     M_out = M;
     L_out = L;
@@ -661,7 +673,9 @@ __device__ __forceinline__ float fold_partials_small(const float* __restrict__ b
 }
 
 // Level-1 -> level-2 merge. grid = (B*16, 32), block = 128 (thread = dim).
-// NMAX >= ceil(NC / 32) selects the one-round fold; 0 the generic one.
+// NMAX >= ceil(NC / 32). The partial loads are issued before the limit is
+// read; no block returns early (stores are predicated), so the compiler
+// cannot sink the loads behind the limit.
 template <bool BATCH, uint32_t NMAX>
 __global__ void __launch_bounds__(128) merge_a_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
@@ -669,29 +683,22 @@ __global__ void __launch_bounds__(128) merge_a_kernel(
     float* __restrict__ partials2) {
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u, s = blockIdx.y;
     const uint32_t d = threadIdx.x;
+    const float* P = partials + (((size_t)slot * kHq + qh) * NC + s) * kPartial;
+    Loaded<NMAX> x;
+    load_partials<NMAX>(P, (size_t)kSplit2 * kPartial, (NC - s + kSplit2 - 1u) / kSplit2, x);
     const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
     const uint32_t nv = n_valid_chunks(limit, C, NC);
-    if (nv == 1u) return;
+    const uint32_t n = s < nv ? (nv - s + kSplit2 - 1u) / kSplit2 : 0u;
+    float M, L;
+    const float A = fold_loaded<NMAX>(x, n, M, L);
     float* pw2 = partials2 + (((size_t)slot * kHq + qh) * kSplit2 + s) * kPartial;
-    if (s >= nv) {
-        if (d == 0u) {
-            pw2[0] = -INFINITY;
-            pw2[1] = 0.f;
+    if (nv > 1u) {
+        if (d == 0u) {  // an empty split (s >= nv) stores {-inf, 0}
+            pw2[0] = M;
+            pw2[1] = L;
         }
-        return;
+        if (s < nv) pw2[2 + d] = A;
     }
-    const float* P = partials + (((size_t)slot * kHq + qh) * NC + s) * kPartial;
-    const uint32_t n = (nv - s + kSplit2 - 1u) / kSplit2;
-    float M, L, A;
-    if constexpr (NMAX > 0u)
-        A = fold_partials_small<NMAX>(P, (size_t)kSplit2 * kPartial, n, M, L);
-    else
-        A = fold_partials(P, (size_t)kSplit2 * kPartial, n, M, L);
-    if (d == 0u) {
-        pw2[0] = M;
-        pw2[1] = L;
-    }
-    pw2[2 + d] = A;
 }
 
 // Level-2 -> out. grid = B*16, block = 128.
@@ -701,32 +708,46 @@ __global__ void __launch_bounds__(128) merge_b_kernel(
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
     uint16_t* __restrict__ out) {
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
+    Loaded<kSplit2> x;
+    load_partials<kSplit2>(partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial,
+                           kPartial, kSplit2, x);
     const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
-    if (n_valid_chunks(limit, C, NC) == 1u) return;
+    const bool active = n_valid_chunks(limit, C, NC) > 1u;
     float M, L;
-    const float A = fold_partials_small<kSplit2>(
-        partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial, kPartial, kSplit2, M, L);
-    out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
+    const float A = fold_loaded<kSplit2>(x, kSplit2, M, L);
+    if (active)
+        out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
 }
 
 // One-level merge of all valid level-1 partials (used when no level-2 buffer
-// is given, or when NC <= 32). grid = B*16, block = 128; NMAX as in merge_a.
+// is given, or when NC <= 32). grid = B*16, block = 128. NMAX >= NC selects
+// the one-round fold (loads before the limit, as in merge_a); 0 the generic
+// fold over up to kMaxFold partials.
 template <bool BATCH, uint32_t NMAX>
 __global__ void __launch_bounds__(128) merge_p_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
     uint16_t* __restrict__ out) {
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
-    const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
-    const uint32_t nv = n_valid_chunks(limit, C, NC);
-    if (nv == 1u) return;
     const float* base = partials + ((size_t)slot * kHq + qh) * NC * kPartial;
     float M, L, A;
-    if constexpr (NMAX > 0u)
-        A = fold_partials_small<NMAX>(base, kPartial, nv, M, L);
-    else
+    bool active;
+    if constexpr (NMAX > 0u) {
+        Loaded<NMAX> x;
+        load_partials<NMAX>(base, kPartial, NC, x);
+        const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
+        const uint32_t nv = n_valid_chunks(limit, C, NC);
+        active = nv > 1u;
+        A = fold_loaded<NMAX>(x, nv, M, L);
+    } else {
+        const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
+        const uint32_t nv = n_valid_chunks(limit, C, NC);
+        if (nv == 1u) return;
+        active = true;
         A = fold_partials(base, kPartial, nv, M, L);
-    out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
+    }
+    if (active)
+        out[((size_t)slot * kHq + qh) * kD + threadIdx.x] = f32_to_bf16(L > 0.f ? A / L : 0.f);
 }
 
 // Chunks per workgroup: enough workgroups for ~kTargetBlocks resident blocks
@@ -785,14 +806,12 @@ mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
     // the one-level fold: a single kernel gives the identical result.
     if (partials2 != nullptr && NC > kSplit2) {
         const dim3 ga(B * kHq, kSplit2);
+        static_assert(kMaxFold <= 64u * kSplit2, "merge_a folds at most 64 per split");
         if (NC <= 16u * kSplit2)
             hipLaunchKernelGGL((merge_a_kernel<BATCH, 16u>), ga, dim3(128), 0, st, partials,
                                d_pos, slot_pos, NC, C, partials2);
-        else if (NC <= 64u * kSplit2)
-            hipLaunchKernelGGL((merge_a_kernel<BATCH, 64u>), ga, dim3(128), 0, st, partials,
-                               d_pos, slot_pos, NC, C, partials2);
         else
-            hipLaunchKernelGGL((merge_a_kernel<BATCH, 0u>), ga, dim3(128), 0, st, partials,
+            hipLaunchKernelGGL((merge_a_kernel<BATCH, 64u>), ga, dim3(128), 0, st, partials,
                                d_pos, slot_pos, NC, C, partials2);
         hipLaunchKernelGGL((merge_b_kernel<BATCH>), dim3(B * kHq), dim3(128), 0, st,
                            partials2, d_pos, slot_pos, NC, C, out);

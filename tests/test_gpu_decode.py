@@ -142,12 +142,15 @@ def test_decode_chunk_tiers(kvm, orc, dev, C, P):
     check_vs_ref(orc, got, ref, f"tier C={C} P={P}")
 
 
-@pytest.mark.parametrize("limit", [257 * 64 - 1, 5 * 64 + 10])
-def test_merge2_synthetic(kvm, orc, dev, limit):
+@pytest.mark.parametrize("N,limit", [(257, 257 * 64 - 1), (257, 5 * 64 + 10),
+                                     (512, 512 * 64 - 1), (512, 33 * 64),
+                                     (2048, 2048 * 64 - 1), (2048, 700 * 64 + 3)])
+def test_merge2_synthetic(kvm, orc, dev, N, limit):
     """Fixed random level-1 partials with l == 0 holes and a poisoned tail
-    (kernel_ops.cpp:2061-2218): two-level merge vs the double oracle."""
+    (kernel_ops.cpp:2061-2218): two-level merge vs the double oracle, with
+    16 (N <= 512) and 64 (N = 2048) chunks per level-2 split."""
     import torch
-    N, C = 257, 64
+    C = 64
     nv = min(limit // C + 1, N)
     lcg = Lcg(0xA12E + (0 if limit > 1000 else 7919))
     parts = np.empty((16, N, 130), dtype=np.float32)
