@@ -9,7 +9,7 @@ the headline workload C4 (one session, 131072 cached tokens in 2048 pages of
 second over the whole timed region (inputs resident in HBM); the other
 configurations are reported under "configs".
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,pf]
 """
 from __future__ import annotations
 
@@ -24,6 +24,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
 LAYERS = 28
 P = 64
 KV_BYTES_PER_TOKEN = 1024  # K+V, 2 kv heads x 128 dims x bf16, one layer
@@ -39,7 +40,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c4,c3,c1,c2")
+    ap.add_argument("--configs", default="c4,c3,c1,c2,pf")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (eager launches)")
@@ -241,7 +242,46 @@ def bench_append(kvm, torch, dev, timer, T, steps, warmup):
         "kv_bytes_per_layer": kv_bytes, "all_bytes_per_layer": kv_bytes + q_bytes,
         "gbs_incl_q": (kv_bytes + q_bytes) / (us * 1e-6) / 1e9,
         "pct_hbm_peak_incl_q": 100.0 * (kv_bytes + q_bytes) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        "tokens_per_s": T * LAYERS / (ms * 1e-3),
+        "tokens_per_s": T / (ms * 1e-3),
+    }
+
+
+def bench_prefill(kvm, torch, dev, timer, T, base, steps, warmup):
+    """Prefill attention (page gather + causal flash attention) of one T-token
+    chunk whose rows sit at positions base..base+T-1, over the paged pool
+    (positions 0..base+T-1 cached), 28 layers. Compute-bound: reported against
+    the dense bf16 MFMA peak; causal flops = 4 * 16 heads * 128 * sum_t (base+t+1)."""
+    ctx = base + T
+    npages = -(-ctx // P)
+    maxp = npages
+    lay = kvm.KvLayout(maxp, P, LAYERS)
+    g = torch.Generator(device="cpu").manual_seed(9)
+    pt = torch.randperm(maxp, generator=g).to(torch.int32).to(dev)
+    pool = make_session_pool(torch, dev, maxp, LAYERS)
+    qs = q_rows(torch, dev, T * LAYERS)
+    d_base = torch.tensor([base], dtype=torch.int32, device=dev)
+    S = kvm.prefill_flash_split_kv(T)
+    parts = torch.empty(max(1, T * 16 * S * 130) if S > 1 else 1, dtype=torch.float32,
+                        device=dev)
+    out = torch.empty(T * 2048, dtype=torch.int16, device=dev)
+
+    def step_f():
+        for l in range(LAYERS):
+            kvm.launch_attn_prefill_flash(qs[l * T * 2560:], T, d_base, l, pt, pool, lay, out,
+                                          parts, S)
+
+    step = timer.capture([step_f])
+    timer.run(step, warmup)
+    ms = timer.run(step, steps)
+    us = ms * 1e3 / LAYERS
+    flops = 4.0 * 16 * 128 * (T * base + T * (T + 1) / 2)
+    kv_bytes = ctx * KV_BYTES_PER_TOKEN + T * 2048 * 2 * 2  # KV once + q read + out write
+    return {
+        "tokens": T, "base": base, "split_kv": S, "us_per_layer": us, "ms_per_step": ms,
+        "tflops": flops / (us * 1e-6) / 1e12,
+        "pct_mfma_bf16_peak": 100.0 * flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "flops_per_layer": flops, "algorithmic_bytes_per_layer": kv_bytes,
+        "tokens_per_s": T / (ms * 1e-3),
     }
 
 
@@ -316,6 +356,15 @@ def main():
                                              args.warmup)
         log(res["c2_append_8448"])
         torch.cuda.empty_cache()
+
+    if "pf" in cfgs:
+        for base in (0, 8448):
+            log(f"prefill attention 8448 tokens at base {base} ...")
+            r = bench_prefill(kvm, torch, dev, timer, 8448, base, max(2, args.steps // 4),
+                              1)
+            res[f"prefill_attn_8448_base{base}"] = r
+            log(r)
+            torch.cuda.empty_cache()
 
     if args.calib:
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
