@@ -15,15 +15,24 @@
 //     partial {m, l, acc} at partials[((t*16 + qh)*S_kv + s)*130] and a merge
 //     kernel (block per (t, qh)) folds the S_kv partials in ascending order.
 //
-// MI355X design: one 256-thread workgroup (4 wave64) per (kv head, 16-row q
-// tile, key split). The 16 rows x 8 query heads of a KV head form 128 query
-// vectors; wave w owns rows 4w..4w+3 as two 16-column groups (column n =
-// head n%8 of row 4w + 2*group + n/8), so every MFMA column is a real query.
-// The key tile is gathered once per workgroup into LDS (double buffered, two
-// 16-byte global loads per thread); each wave then computes
-// S^T = K x Q^T (v_mfma_f32_16x16x32_bf16), the online softmax per column,
-// transposes V with an identity MFMA and accumulates O^T += V^T x P^T
-// (v_mfma_f32_16x16x16bf16_1k), the same operand scheme as the decode kernel.
+// MI355X design: one 512-thread workgroup (8 wave64, 2 per SIMD) per (kv
+// head, 32-row q tile, key split); heavy (late) q tiles are launched first.
+// The 32 rows x 8 query heads of a KV head are 256 query vectors: wave w owns
+// two 16-column groups, group g holding rows 4w + 2g + {0, 1} x heads 0..7. Keys stream in
+// 32-position steps gathered through the page table into LDS (double
+// buffered, register-staged prefetch of the next step): K row-major, V
+// transposed (dims x keys) so that both MFMA operands are contiguous LDS
+// reads. Per step and column group:
+//   * S^T = K x Q^T: 2 key blocks x 4 v_mfma_f32_16x16x32_bf16 (Q^T in
+//     registers for the whole kernel);
+//   * online softmax per column over the 32 keys (lane holds 8 scores, two
+//     cross-lane xor steps), p fp32 for l, bf16 for P.V;
+//   * O^T += V^T x P^T: 8 v_mfma_f32_16x16x32_bf16 over the 32 keys, with
+//     the contraction index permuted identically on both operands so that
+//     P^T is exactly the lanes' softmax output.
+// The online-softmax update runs per 32 keys (the reference updates per 16)
+// with a lazily moved reference max; both are exact restatements of softmax
+// and differ only in rounding.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -36,219 +45,243 @@ namespace mckv {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kThreads = 256;
-constexpr uint32_t kPitch = 136;  // LDS row pitch (bf16) of a 128-dim row
+constexpr uint32_t kThreads = 512;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) {
     return __builtin_bit_cast(bf16x8, u);
 }
-__device__ __forceinline__ s16x4 as_s16x4(const uint2& u) {
-    return __builtin_bit_cast(s16x4, u);
-}
-__device__ __forceinline__ s16x4 trunc_bf16x4(const f32x4& t) {
-    uint2 r;
-    r.x = (__float_as_uint(t[0]) >> 16) | (__float_as_uint(t[1]) & 0xFFFF0000u);
-    r.y = (__float_as_uint(t[2]) >> 16) | (__float_as_uint(t[3]) & 0xFFFF0000u);
-    return __builtin_bit_cast(s16x4, r);
-}
+constexpr uint32_t kQRows = 32;  // q rows per workgroup
+constexpr uint32_t kStep = 32;   // keys per step
+constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
+constexpr uint32_t kVPitch = 36;   // sVt row pitch (bf16): 32 keys + 4
 
 __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     const uint16_t* __restrict__ q_rows, uint32_t T,
     const uint32_t* __restrict__ d_base_pos, uint32_t layer,
     const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
     uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S) {
-    __shared__ __align__(16) uint16_t sK[2][16 * kPitch];
-    __shared__ __align__(16) uint16_t sV[2][16 * kPitch];
+    __shared__ __align__(16) uint16_t sK[2][kStep * kKPitch];
+    __shared__ __align__(16) uint16_t sVt[2][kD * kVPitch];
 
-    const uint32_t ntq = (T + 15u) / 16u;
+    const uint32_t ntq = (T + kQRows - 1u) / kQRows;
     const uint32_t s = blockIdx.x % S;
-    const uint32_t qt = (blockIdx.x / S) % ntq;
-    const uint32_t kvh = (blockIdx.x / S) / ntq;
-    const uint32_t tb = qt * 16u;
+    const uint32_t kvh = (blockIdx.x / S) % kHkv;
+    const uint32_t qt = ntq - 1u - blockIdx.x / (S * kHkv);  // heavy tiles first
+    const uint32_t tb = qt * kQRows;
     const uint32_t base_pos = *d_base_pos;
-    const uint32_t key_end = base_pos + tb + min(15u, T - 1u - tb);  // last key
-    const uint32_t last = key_end >> 4;
+    const uint32_t key_end = base_pos + tb + min(kQRows - 1u, T - 1u - tb);  // last key
+    const uint32_t last = key_end / kStep;
     const uint32_t qsp = (last + S) / S;  // ceil((last+1)/S)
-    const uint32_t jt0 = s * qsp;
-    const uint32_t jt1 = min(jt0 + qsp - 1u, last);
+    const uint32_t js0 = s * qsp;
+    const uint32_t js1 = min(js0 + qsp - 1u, last);
 
     const uint32_t tid = threadIdx.x;
-    const uint32_t wave = tid >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lane = tid & 63u;
     const uint32_t col = lane & 15u;
     const uint32_t grp = lane >> 4;
+    constexpr int G = 2;
 
     // Query columns: group g, column col -> head col%8, row 4*wave + 2g + col/8.
-    uint32_t row[2];
-    bf16x8 qb[2][4];
+    uint32_t row[G];
+    bf16x8 qb[G][4];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
+    for (int g = 0; g < G; ++g) {
         row[g] = tb + 4u * wave + 2u * g + (col >> 3);
         const bool ok = row[g] < T;
         const uint16_t* q =
-            q_rows + (size_t)(ok ? row[g] : 0u) * kRow + (kvh * kGroup + (col & 7u)) * kD +
+            q_rows + (size_t)(ok ? row[g] : tb) * kRow + (kvh * kGroup + (col & 7u)) * kD +
             8u * grp;
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-            qb[g][m] = as_bf16x8(ok ? *reinterpret_cast<const uint4*>(q + 32u * m)
-                                    : make_uint4(0u, 0u, 0u, 0u));
+        for (int m = 0; m < 4; ++m) {
+            const uint4 v = *reinterpret_cast<const uint4*>(q + 32u * m);
+            qb[g][m] = as_bf16x8(ok ? v : make_uint4(0u, 0u, 0u, 0u));
+        }
     }
-    s16x4 ident;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        ident[i] = (4u * grp + (uint32_t)i == col) ? (short)0x3F80 : (short)0;
 
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-    f32x4 acc[2][4][2];
+    float m_run[G], l_run[G], ren[G];
+    f32x4 acc[G][8];
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int g = 0; g < G; ++g) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.f;
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) acc[g][m][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int db = 0; db < 8; ++db) acc[g][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
-    // Cooperative gather: element idx = tid + 256*r covers (pos sp, K/V, 8 dims).
+    // Cooperative gather, 2 chunks of 16 bytes per thread: the K chunk of key
+    // tid/16, dims 8*(tid%16), and the V chunk of key tid%32, dims 8*(tid/32)
+    // (so that the transposed LDS stores of a wave hit consecutive keys of one
+    // dim row).
     uint4 stage[2];
-    auto gather = [&](uint32_t jt) {
+    const uint32_t kkey = tid >> 4, kdb = tid & 15u, vkey = tid & 31u, vdb = tid >> 5;
+    auto gather = [&](uint32_t js) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const uint32_t idx = tid + 256u * r;
-            const uint32_t sp = idx >> 5, w4 = idx & 31u;
-            const uint32_t pos = jt * 16u + sp;
+            const uint32_t key = r ? vkey : kkey, dblk = r ? vdb : kdb;
+            const uint32_t pos = js * kStep + key;
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
+#ifdef PF_NO_GATHER
+            if (pos == 0xFFFFFFFFu) {
+#else
             if (pos <= key_end) {
+#endif
                 const uint32_t page = pt[pos >> ly.log2p];
                 v = *reinterpret_cast<const uint4*>(
-                    pool + token_base(ly, layer, page, pos & ly.pmask) +
-                    (w4 >> 4) * 256u + kvh * kD + (w4 & 15u) * 8u);
+                    pool + token_base(ly, layer, page, pos & ly.pmask) + (r ? 256u : 0u) +
+                    kvh * kD + dblk * 8u);
             }
             stage[r] = v;
         }
     };
     auto put = [&](int b) {
+        *reinterpret_cast<uint4*>(&sK[b][kkey * kKPitch + kdb * 8u]) = stage[0];
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&stage[1]);
+        uint16_t* dst = &sVt[b][vdb * 8u * kVPitch + vkey];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const uint32_t idx = tid + 256u * r;
-            const uint32_t sp = idx >> 5, w4 = idx & 31u;
-            uint16_t* dst = ((w4 >> 4) ? sV[b] : sK[b]) + sp * kPitch + (w4 & 15u) * 8u;
-            *reinterpret_cast<uint4*>(dst) = stage[r];
-        }
+        for (int i = 0; i < 8; ++i) dst[i * kVPitch] = e[i];
     };
 
-    if (jt0 <= jt1) gather(jt0);
+    // exp(score - m) = exp2(s*c - m*c) with s the raw dot product, c = scale *
+    // log2(e): one FMA and one v_exp per score. m_run is the running max of the
+    // raw scores (c > 0). l is kept per lane (its own 8 keys per step) and
+    // summed across the 4 lane groups at the end.
+    constexpr float kC = kScoreScale * 1.4426950408889634f;
+    if (js0 <= js1) gather(js0);
     int b = 0;
-    for (uint32_t jt = jt0; jt <= jt1; ++jt, b ^= 1) {
+    for (uint32_t js = js0; js <= js1; ++js, b ^= 1) {
         put(b);
         __syncthreads();
-        if (jt < jt1) gather(jt + 1u);
+        if (js < js1) gather(js + 1u);
         const uint16_t* K = sK[b];
-        const uint16_t* V = sV[b];
-        // K tile as A operand: lane (pos = col, grp) holds dims 32m + 8*grp + 0..7.
-        bf16x8 ka[4];
+        const uint16_t* Vt = sVt[b];
+#ifdef PF_NO_COMPUTE
+        if (K[tid] == 0x1234u) l_run[0] += 1.f;
+        continue;
+#endif
+        // S^T blocks: key block kb (keys 16kb + row), lane col = query column.
+        f32x4 sacc[2][G];
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-            ka[m] = as_bf16x8(*reinterpret_cast<const uint4*>(K + col * kPitch + 32u * m +
-                                                              8u * grp));
-        // V^T blocks via identity MFMA (shared by both column groups).
-        s16x4 vt[4][2];
+        for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+            for (int g = 0; g < G; ++g) sacc[kb][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint2 raw = *reinterpret_cast<const uint2*>(
-                    V + col * kPitch + 32u * m + 8u * grp + 4u * h);
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                vt[m][h] = trunc_bf16x4(
-                    __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s16x4(raw), ident, z, 0,
-                                                              0, 0));
+            for (int m = 0; m < 4; ++m) {
+                const bf16x8 ka = as_bf16x8(*reinterpret_cast<const uint4*>(
+                    K + (16u * kb + col) * kKPitch + 32u * m + 8u * grp));
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    sacc[kb][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[g][m],
+                                                                          sacc[kb][g], 0, 0, 0);
             }
-        const uint32_t pos0 = jt * 16u + 4u * grp;
+        }
+        // Keys of this lane: 32*js + 16*kb + 4*grp + j. Only steps that reach
+        // past the tile's first row can hold masked keys (wave-uniform test).
+        if (js * kStep + kStep - 1u > base_pos + tb) {
+            const uint32_t pos0 = js * kStep + 4u * grp;
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+            for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
-                sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[m], qb[g][m], sacc, 0, 0,
-                                                               0);
-            const uint32_t lim = base_pos + row[g];
-            float sc[4];
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float v;
-                {
-#pragma clang fp contract(off)
-                    v = sacc[j] * kScoreScale;
-                }
-                sc[j] = (pos0 + (uint32_t)j <= lim) ? v : -INFINITY;
-            }
-            float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                    for (int j = 0; j < 4; ++j)
+                        if (pos0 + 16u * kb + (uint32_t)j > base_pos + row[g])
+                            sacc[kb][g][j] = -INFINITY;
+        }
+        bf16x8 pb[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float tm = fmaxf(fmaxf(fmaxf(sacc[0][g][0], sacc[0][g][1]),
+                                   fmaxf(sacc[0][g][2], sacc[0][g][3])),
+                             fmaxf(fmaxf(sacc[1][g][0], sacc[1][g][1]),
+                                   fmaxf(sacc[1][g][2], sacc[1][g][3])));
             tm = fmaxf(tm, __shfl_xor(tm, 16));
             tm = fmaxf(tm, __shfl_xor(tm, 32));
-            float mn = fmaxf(m_run[g], tm);
-            const float renew = (m_run[g] == -INFINITY) ? 0.f : __expf(m_run[g] - mn);
-            const float mnext = mn;
-            if (mn == -INFINITY) mn = 0.f;  // fully masked so far: p = 0, state kept
-            float p[4];
+            const float mn = fmaxf(m_run[g], tm);
+            // Lazy reference point: m_run moves only when the new max exceeds
+            // it by more than 8 in log2 units (p <= 2^8 otherwise) or when it
+            // is still -inf; softmax is invariant to the reference point, so
+            // this changes rounding only and leaves most steps without the
+            // acc rescale. Column-uniform (mn, m_run agree across lane groups).
+            const bool move = (m_run[g] == -INFINITY) ? (mn != -INFINITY)
+                                                     : ((mn - m_run[g]) * kC > 8.f);
+            ren[g] = 1.f;
+            if (move) {
+                const float renew =
+                    (m_run[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run[g] - mn) * kC);
+                l_run[g] *= renew;
+                m_run[g] = mn;
+                ren[g] = renew;
+            }
+            // fully masked so far (m_run = -inf): p = 0 and the state is kept
+            const float nmc = (m_run[g] == -INFINITY) ? 0.f : -m_run[g] * kC;
+            float ls = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) p[j] = __expf(sc[j] - mn);
-            float ls = (p[0] + p[1]) + (p[2] + p[3]);
-            ls += __shfl_xor(ls, 16);
-            ls += __shfl_xor(ls, 32);
-            l_run[g] = l_run[g] * renew + ls;
-            m_run[g] = mnext;
-            s16x4 pb;
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) pb[j] = (short)f32_to_bf16(p[j]);
-#pragma unroll
-            for (int m = 0; m < 4; ++m)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    acc[g][m][h] = acc[g][m][h] * renew;
-                    acc[g][m][h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                        vt[m][h], pb, acc[g][m][h], 0, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][g][j], kC, nmc));
+                    ls += p;
+                    pb[g][4 * kb + j] = (__bf16)p;
                 }
+            l_run[g] += ls;
+            if (__builtin_amdgcn_ballot_w64(ren[g] != 1.f) != 0u) {
+#pragma unroll
+                for (int db = 0; db < 8; ++db) acc[g][db] = acc[g][db] * ren[g];
+            }
+        }
+        // O^T += V^T x P^T; contraction index i of lane group grp <-> key
+        // 16*(i/4) + 4*grp + i%4 on both operands.
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const uint16_t* vr = Vt + (16u * db + col) * kVPitch + 4u * grp;
+            const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16u);
+            const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                acc[g][db] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g], acc[g][db], 0, 0, 0);
         }
     }
-
-    // Epilogue: lane holds dims 32m + 8*grp + 4h + j of column (head, row).
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
+    for (int g = 0; g < G; ++g) {
+        l_run[g] += __shfl_xor(l_run[g], 16);
+        l_run[g] += __shfl_xor(l_run[g], 32);
+    }
+
+    // Epilogue: lane holds dims 16*db + 4*grp + j of column (head, row).
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
         if (row[g] >= T) continue;
         const uint32_t qh = kvh * kGroup + (col & 7u);
         if (S == 1u) {
-            uint16_t* o = out + (size_t)row[g] * 2048u + qh * kD + 8u * grp;
+            uint16_t* o = out + (size_t)row[g] * 2048u + qh * kD + 4u * grp;
             const float L = l_run[g];
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
+            for (int db = 0; db < 8; ++db) {
+                uint16_t w[4];
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    uint16_t w[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        w[j] = f32_to_bf16(L > 0.f ? acc[g][m][h][j] / L : 0.f);
-                    *reinterpret_cast<uint2*>(o + 32u * m + 4u * h) =
-                        make_uint2((uint32_t)w[0] | ((uint32_t)w[1] << 16),
-                                   (uint32_t)w[2] | ((uint32_t)w[3] << 16));
-                }
+                for (int j = 0; j < 4; ++j)
+                    w[j] = f32_to_bf16(L > 0.f ? acc[g][db][j] / L : 0.f);
+                *reinterpret_cast<uint2*>(o + 16u * db) =
+                    make_uint2((uint32_t)w[0] | ((uint32_t)w[1] << 16),
+                               (uint32_t)w[2] | ((uint32_t)w[3] << 16));
+            }
         } else {
             float* pw = partials + ((size_t)(row[g] * 16u + qh) * S + s) * kPartial;
-            if (grp == 0u) {
-                pw[0] = m_run[g];
+            if (grp == 0u) {  // m of the record is in score units (raw * scale)
+                pw[0] = m_run[g] * kScoreScale;
                 pw[1] = l_run[g];
             }
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    float* d = pw + 2u + 32u * m + 8u * grp + 4u * h;
-                    *reinterpret_cast<float2*>(d) =
-                        make_float2(acc[g][m][h][0], acc[g][m][h][1]);
-                    *reinterpret_cast<float2*>(d + 2) =
-                        make_float2(acc[g][m][h][2], acc[g][m][h][3]);
-                }
+            for (int db = 0; db < 8; ++db) {
+                float* d = pw + 2u + 16u * db + 4u * grp;
+                *reinterpret_cast<float2*>(d) = make_float2(acc[g][db][0], acc[g][db][1]);
+                *reinterpret_cast<float2*>(d + 2) = make_float2(acc[g][db][2], acc[g][db][3]);
+            }
         }
     }
 }
@@ -300,7 +333,7 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
                   tokens, S_kv, (void*)d_partials);
         return MC_E_INVALID_ARGUMENT;
     }
-    const uint32_t ntq = (tokens + 15u) / 16u;
+    const uint32_t ntq = (tokens + kQRows - 1u) / kQRows;
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(prefill_attn_kernel, dim3(kHkv * ntq * S_kv), dim3(kThreads), 0,
                        st, d_q_rows, tokens, d_base_pos, layer, d_page_table, d_kv_pool,
