@@ -53,10 +53,17 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) {
     return __builtin_bit_cast(bf16x8, u);
 }
 constexpr uint32_t kQRows = 32;  // q rows per workgroup
-constexpr uint32_t kStep = 32;   // keys per step
+#ifndef PF_STEP
+#define PF_STEP 64
+#endif
+constexpr uint32_t kStep = PF_STEP;  // keys per step (32 or 64)
+constexpr int kNKB = kStep / 16;     // 16-key blocks per step
+constexpr int kNH = kStep / 32;      // 32-key halves per step (one PV MFMA each)
+static_assert(kStep == 32 || kStep == 64, "step of 32 or 64 keys");
 constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
-constexpr uint32_t kVPitch = 36;   // sVt row pitch (bf16): 32 keys + 4
+constexpr uint32_t kVPitch = kStep + 4;  // sVt row pitch (bf16): keys + 4
 
+template <bool PAGE_STEP>
 __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     const uint16_t* __restrict__ q_rows, uint32_t T,
     const uint32_t* __restrict__ d_base_pos, uint32_t layer,
@@ -115,12 +122,34 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     // tid/16, dims 8*(tid%16), and the V chunk of key tid%32, dims 8*(tid/32)
     // (so that the transposed LDS stores of a wave hit consecutive keys of one
     // dim row).
-    uint4 stage[2];
+    uint4 stage[2 * kNH];  // [K chunks of each half, then V chunks]
     const uint32_t kkey = tid >> 4, kdb = tid & 15u, vkey = tid & 31u, vdb = tid >> 5;
-    auto gather = [&](uint32_t js) {
+    // Page ids are fetched one step ahead of the K/V loads that use them, so
+    // a gather waits for one memory latency, not two. With P >= kStep a step lies
+    // in one page and its id is read through the scalar path.
+    auto page_ids = [&](uint32_t js, uint32_t (&pg)[2 * kNH]) {
+        if constexpr (PAGE_STEP) {
+            const uint32_t pos = js * kStep;
+            const uint32_t id = pos <= key_end
+                                    ? ((const __attribute__((address_space(4))) uint32_t*)(pt))
+                                          [__builtin_amdgcn_readfirstlane(pos >> ly.log2p)]
+                                    : 0u;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const uint32_t key = r ? vkey : kkey, dblk = r ? vdb : kdb;
+            for (int r = 0; r < 2 * kNH; ++r) pg[r] = id;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 2 * kNH; ++r) {
+                const uint32_t pos = js * kStep + 32u * (r % kNH) + (r >= kNH ? vkey : kkey);
+                pg[r] = pos <= key_end ? pt[pos >> ly.log2p] : 0u;
+            }
+        }
+    };
+    auto gather = [&](uint32_t js, const uint32_t (&pg)[2 * kNH]) {
+#pragma unroll
+        for (int r = 0; r < 2 * kNH; ++r) {
+            const bool isv = r >= kNH;
+            const uint32_t key = 32u * (r % kNH) + (isv ? vkey : kkey);
+            const uint32_t dblk = isv ? vdb : kdb;
             const uint32_t pos = js * kStep + key;
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
 #ifdef PF_NO_GATHER
@@ -128,20 +157,22 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
 #else
             if (pos <= key_end) {
 #endif
-                const uint32_t page = pt[pos >> ly.log2p];
                 v = *reinterpret_cast<const uint4*>(
-                    pool + token_base(ly, layer, page, pos & ly.pmask) + (r ? 256u : 0u) +
+                    pool + token_base(ly, layer, pg[r], pos & ly.pmask) + (isv ? 256u : 0u) +
                     kvh * kD + dblk * 8u);
             }
             stage[r] = v;
         }
     };
     auto put = [&](int b) {
-        *reinterpret_cast<uint4*>(&sK[b][kkey * kKPitch + kdb * 8u]) = stage[0];
-        const uint16_t* e = reinterpret_cast<const uint16_t*>(&stage[1]);
-        uint16_t* dst = &sVt[b][vdb * 8u * kVPitch + vkey];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dst[i * kVPitch] = e[i];
+        for (int h = 0; h < kNH; ++h) {
+            *reinterpret_cast<uint4*>(&sK[b][(32u * h + kkey) * kKPitch + kdb * 8u]) = stage[h];
+            const uint16_t* e = reinterpret_cast<const uint16_t*>(&stage[kNH + h]);
+            uint16_t* dst = &sVt[b][vdb * 8u * kVPitch + 32u * h + vkey];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dst[i * kVPitch] = e[i];
+        }
     };
 
     // exp(score - m) = exp2(s*c - m*c) with s the raw dot product, c = scale *
@@ -149,12 +180,20 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     // raw scores (c > 0). l is kept per lane (its own 8 keys per step) and
     // summed across the 4 lane groups at the end.
     constexpr float kC = kScoreScale * 1.4426950408889634f;
-    if (js0 <= js1) gather(js0);
+    uint32_t pgn[2 * kNH] = {};
+    if (js0 <= js1) {
+        page_ids(js0, pgn);
+        gather(js0, pgn);
+        if (js0 < js1) page_ids(js0 + 1u, pgn);
+    }
     int b = 0;
     for (uint32_t js = js0; js <= js1; ++js, b ^= 1) {
         put(b);
         __syncthreads();
-        if (js < js1) gather(js + 1u);
+        if (js < js1) {
+            gather(js + 1u, pgn);
+            if (js + 1u < js1) page_ids(js + 2u, pgn);
+        }
         const uint16_t* K = sK[b];
         const uint16_t* Vt = sVt[b];
 #ifdef PF_NO_COMPUTE
@@ -162,9 +201,9 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         continue;
 #endif
         // S^T blocks: key block kb (keys 16kb + row), lane col = query column.
-        f32x4 sacc[2][G];
+        f32x4 sacc[kNKB][G];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < kNKB; ++kb) {
 #pragma unroll
             for (int g = 0; g < G; ++g) sacc[kb][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -184,19 +223,20 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
 #pragma unroll
             for (int g = 0; g < G; ++g)
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < kNKB; ++kb)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         if (pos0 + 16u * kb + (uint32_t)j > base_pos + row[g])
                             sacc[kb][g][j] = -INFINITY;
         }
-        bf16x8 pb[G];
+        bf16x8 pb[G][kNH];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            float tm = fmaxf(fmaxf(fmaxf(sacc[0][g][0], sacc[0][g][1]),
-                                   fmaxf(sacc[0][g][2], sacc[0][g][3])),
-                             fmaxf(fmaxf(sacc[1][g][0], sacc[1][g][1]),
-                                   fmaxf(sacc[1][g][2], sacc[1][g][3])));
+            float tm = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < kNKB; ++kb)
+                tm = fmaxf(tm, fmaxf(fmaxf(sacc[kb][g][0], sacc[kb][g][1]),
+                                     fmaxf(sacc[kb][g][2], sacc[kb][g][3])));
             tm = fmaxf(tm, __shfl_xor(tm, 16));
             tm = fmaxf(tm, __shfl_xor(tm, 32));
             const float mn = fmaxf(m_run[g], tm);
@@ -219,12 +259,12 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
             const float nmc = (m_run[g] == -INFINITY) ? 0.f : -m_run[g] * kC;
             float ls = 0.f;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < kNKB; ++kb)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][g][j], kC, nmc));
                     ls += p;
-                    pb[g][4 * kb + j] = (__bf16)p;
+                    pb[g][kb >> 1][4 * (kb & 1) + j] = (__bf16)p;
                 }
             l_run[g] += ls;
             if (__builtin_amdgcn_ballot_w64(ren[g] != 1.f) != 0u) {
@@ -232,19 +272,21 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
                 for (int db = 0; db < 8; ++db) acc[g][db] = acc[g][db] * ren[g];
             }
         }
-        // O^T += V^T x P^T; contraction index i of lane group grp <-> key
-        // 16*(i/4) + 4*grp + i%4 on both operands.
+        // O^T += V^T x P^T per 32-key half h; contraction index i of lane
+        // group grp <-> key 32h + 16*(i/4) + 4*grp + i%4 on both operands.
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const uint16_t* vr = Vt + (16u * db + col) * kVPitch + 4u * grp;
-            const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-            const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16u);
-            const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+        for (int h = 0; h < kNH; ++h)
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-                acc[g][db] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g], acc[g][db], 0, 0, 0);
-        }
+            for (int db = 0; db < 8; ++db) {
+                const uint16_t* vr = Vt + (16u * db + col) * kVPitch + 32u * h + 4u * grp;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16u);
+                const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    acc[g][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g][h],
+                                                                         acc[g][db], 0, 0, 0);
+            }
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -335,9 +377,14 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
     }
     const uint32_t ntq = (tokens + kQRows - 1u) / kQRows;
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(prefill_attn_kernel, dim3(kHkv * ntq * S_kv), dim3(kThreads), 0,
-                       st, d_q_rows, tokens, d_base_pos, layer, d_page_table, d_kv_pool,
-                       ly, d_out, d_partials, S_kv);
+    if ((1u << ly.log2p) >= kStep)
+        hipLaunchKernelGGL(prefill_attn_kernel<true>, dim3(kHkv * ntq * S_kv), dim3(kThreads),
+                           0, st, d_q_rows, tokens, d_base_pos, layer, d_page_table,
+                           d_kv_pool, ly, d_out, d_partials, S_kv);
+    else
+        hipLaunchKernelGGL(prefill_attn_kernel<false>, dim3(kHkv * ntq * S_kv),
+                           dim3(kThreads), 0, st, d_q_rows, tokens, d_base_pos, layer,
+                           d_page_table, d_kv_pool, ly, d_out, d_partials, S_kv);
     if (S_kv > 1u)
         hipLaunchKernelGGL(prefill_merge_kernel, dim3(tokens * 16u), dim3(128), 0, st,
                            d_partials, S_kv, tokens, d_out);

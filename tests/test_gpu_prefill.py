@@ -77,3 +77,15 @@ def test_prefill_split_kv(kvm, orc, dev, T, S):
 def test_prefill_cross_chunk_8448_prefix(kvm, orc, dev):
     """Second prefill chunk after an 8448-token prefix, 64-token pages."""
     run_prefill(kvm, orc, dev, 96, 8448, 1, P=64, seed=11)
+
+
+@pytest.mark.parametrize("P,S", [(8, 1), (16, 2), (1, 1)])
+def test_prefill_small_pages(kvm, orc, dev, P, S):
+    """Pages smaller than a 32-key step: page ids looked up per key."""
+    run_prefill(kvm, orc, dev, 150, 29, S, P=P, seed=P)
+
+
+def test_prefill_long_chunk(kvm, orc, dev):
+    """2048 rows over a 300-token prefix: many steps per tile, reference max
+    moving late in long rows."""
+    run_prefill(kvm, orc, dev, 2048, 300, 1, P=64, seed=21)
