@@ -62,6 +62,7 @@ constexpr int kNH = kStep / 32;      // 32-key halves per step (one PV MFMA each
 static_assert(kStep == 32 || kStep == 64, "step of 32 or 64 keys");
 constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
 constexpr uint32_t kVPitch = kStep + 4;  // sVt row pitch (bf16): keys + 4
+constexpr uint32_t kBufs = 3;            // LDS K/V buffers (see the ping-pong)
 
 template <bool PAGE_STEP>
 __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
@@ -69,8 +70,8 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     const uint32_t* __restrict__ d_base_pos, uint32_t layer,
     const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
     uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S) {
-    __shared__ __align__(16) uint16_t sK[2][kStep * kKPitch];
-    __shared__ __align__(16) uint16_t sVt[2][kD * kVPitch];
+    __shared__ __align__(16) uint16_t sK[kBufs][kStep * kKPitch];
+    __shared__ __align__(16) uint16_t sVt[kBufs][kD * kVPitch];
 
     const uint32_t ntq = (T + kQRows - 1u) / kQRows;
     const uint32_t s = blockIdx.x % S;
@@ -186,8 +187,33 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         gather(js0, pgn);
         if (js0 < js1) page_ids(js0 + 1u, pgn);
     }
+    // Ping-pong: waves 4..7 (the second wave on each SIMD) add step j's P.V
+    // at the start of step j+1, so that on every SIMD one wave runs MFMA
+    // while the other runs the softmax. Three LDS buffers keep step j's V
+    // intact until then (a wave that writes step j+1's buffer has passed the
+    // barrier of step j, so all waves have finished step j-1).
+    const bool late_pv = wave >= 4u;
+    bf16x8 pb_prev[G][kNH];
+    int bprev = 0;
+    auto pv = [&](const uint16_t* Vt, const bf16x8 (&pbv)[G][kNH]) {
+        // O^T += V^T x P^T per 32-key half h; contraction index i of lane
+        // group grp <-> key 32h + 16*(i/4) + 4*grp + i%4 on both operands.
+#pragma unroll
+        for (int h = 0; h < kNH; ++h)
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const uint16_t* vr = Vt + (16u * db + col) * kVPitch + 32u * h + 4u * grp;
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16u);
+                const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    acc[g][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pbv[g][h],
+                                                                         acc[g][db], 0, 0, 0);
+            }
+    };
     int b = 0;
-    for (uint32_t js = js0; js <= js1; ++js, b ^= 1) {
+    for (uint32_t js = js0; js <= js1; ++js, bprev = b, b = (b + 1 == (int)kBufs) ? 0 : b + 1) {
         put(b);
         __syncthreads();
         if (js < js1) {
@@ -196,6 +222,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         }
         const uint16_t* K = sK[b];
         const uint16_t* Vt = sVt[b];
+        if (late_pv && js > js0) pv(sVt[bprev], pb_prev);
 #ifdef PF_NO_COMPUTE
         if (K[tid] == 0x1234u) l_run[0] += 1.f;
         continue;
@@ -272,22 +299,16 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
                 for (int db = 0; db < 8; ++db) acc[g][db] = acc[g][db] * ren[g];
             }
         }
-        // O^T += V^T x P^T per 32-key half h; contraction index i of lane
-        // group grp <-> key 32h + 16*(i/4) + 4*grp + i%4 on both operands.
+        if (late_pv) {
 #pragma unroll
-        for (int h = 0; h < kNH; ++h)
+            for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int db = 0; db < 8; ++db) {
-                const uint16_t* vr = Vt + (16u * db + col) * kVPitch + 32u * h + 4u * grp;
-                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16u);
-                const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                for (int g = 0; g < G; ++g)
-                    acc[g][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g][h],
-                                                                         acc[g][db], 0, 0, 0);
-            }
+                for (int h = 0; h < kNH; ++h) pb_prev[g][h] = pb[g][h];
+        } else {
+            pv(Vt, pb);
+        }
     }
+    if (late_pv && js0 <= js1) pv(sVt[bprev], pb_prev);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         l_run[g] += __shfl_xor(l_run[g], 16);
