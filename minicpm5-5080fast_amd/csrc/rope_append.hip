@@ -51,11 +51,30 @@ __global__ void __launch_bounds__(256) rope_append_kernel(
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t t = blockIdx.x * kWaves + wave;
     const bool active = t < tokens;
-    const uint32_t pos = *d_base_pos + t;
+    const uint32_t g = lane >> 3;  // head group 0..7
+    const uint32_t j = lane & 7u;  // 8-dim block within the half head
+    // Loads are issued in the order their results are needed and none waits
+    // for another: inv_freq (vector), then the row (6 x 16 bytes per lane;
+    // an inactive wave reads token 0's row, lanes past head 19 re-read head
+    // 19), while the base position and the page id come through the scalar
+    // path. The cos/sin evaluation then overlaps the row loads.
+    typedef const __attribute__((address_space(4))) uint32_t* scalar_u32p;
+    const float f = inv_freq != nullptr ? inv_freq[lane]
+                                        : (float)pow((double)theta, -(double)lane / 64.0);
+    uint16_t* row = qkv + (size_t)(active ? t : 0u) * kRow;
+    uint4 lo[3], hi[3];
+#pragma unroll
+    for (uint32_t it = 0; it < 3; ++it) {
+        const uint32_t h = min(g + 8u * it, 19u);  // 0..15 q, 16..17 k, 18..19 v
+        const uint16_t* src = row + h * 128u;  // q, k and v heads are contiguous
+        lo[it] = *reinterpret_cast<const uint4*>(src + 8u * j);
+        hi[it] = *reinterpret_cast<const uint4*>(src + 64u + 8u * j);
+    }
+    const uint32_t base = *(scalar_u32p)d_base_pos;
+    const uint32_t pos = base + t;
+    const uint32_t tok_pos = __builtin_amdgcn_readfirstlane(active ? pos : base);
+    const uint32_t page = ((scalar_u32p)page_table)[tok_pos >> ly.log2p];
     {
-        const float f = inv_freq != nullptr
-                            ? inv_freq[lane]
-                            : (float)pow((double)theta, -(double)lane / 64.0);
         float c, s;
         rope_sincos((float)pos * f, &c, &s);
         s_cs[wave][lane] = c;
@@ -64,35 +83,29 @@ __global__ void __launch_bounds__(256) rope_append_kernel(
     __syncthreads();
     if (!active) return;
 
-    const uint32_t g = lane >> 3;  // head group 0..7
-    const uint32_t j = lane & 7u;  // 8-dim block within the half head
     float cs[8], sn[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         cs[i] = s_cs[wave][8u * j + i];
         sn[i] = s_sn[wave][8u * j + i];
     }
-    uint16_t* row = qkv + (size_t)t * kRow;
-    const uint32_t page = page_table[pos >> ly.log2p];
     uint16_t* dst = pool + token_base(ly, layer, page, pos & ly.pmask);
 
 #pragma unroll
     for (uint32_t it = 0; it < 3; ++it) {
-        const uint32_t h = g + 8u * it;  // 0..15 q, 16..17 k, 18..19 v
+        const uint32_t h = g + 8u * it;
         if (h >= 20u) break;
-        uint16_t* src = row + h * 128u;  // q, k and v heads are contiguous
-        const uint4 lo = *reinterpret_cast<const uint4*>(src + 8u * j);
-        const uint4 hi = *reinterpret_cast<const uint4*>(src + 64u + 8u * j);
+        uint16_t* src = row + h * 128u;
         if (h < 18u) {
             uint4 olo, ohi;
-            rotate8(lo, hi, cs, sn, olo, ohi);
+            rotate8(lo[it], hi[it], cs, sn, olo, ohi);
             uint16_t* o = (h < 16u) ? src : dst + (h - 16u) * 128u;
             *reinterpret_cast<uint4*>(o + 8u * j) = olo;
             *reinterpret_cast<uint4*>(o + 64u + 8u * j) = ohi;
         } else {
             uint16_t* o = dst + 256u + (h - 18u) * 128u;
-            *reinterpret_cast<uint4*>(o + 8u * j) = lo;
-            *reinterpret_cast<uint4*>(o + 64u + 8u * j) = hi;
+            *reinterpret_cast<uint4*>(o + 8u * j) = lo[it];
+            *reinterpret_cast<uint4*>(o + 64u + 8u * j) = hi[it];
         }
     }
 }
