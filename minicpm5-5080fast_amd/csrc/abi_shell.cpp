@@ -62,7 +62,22 @@ struct DevState {
 
 size_t align256(size_t x) { return (x + 255u) & ~size_t(255); }
 
+// One captured decode step: the per-layer launches of a step are recorded
+// into a HIP graph once and replayed; positions and tokens are read from
+// device memory, so replays need no re-capture.
+struct StepGraph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+void destroy_graph(StepGraph& g) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (g.graph) (void)hipGraphDestroy(g.graph);
+    g = StepGraph{};
+}
+
 struct ModelImpl {
+    bool use_graphs = false;  // mc_model_options_t::enable_cuda_graph
     int device_id = 0;
     uint32_t max_sessions = 0;
     uint32_t max_ctx = 0;
@@ -98,6 +113,8 @@ struct SessionImpl {
     int32_t h_tok = 0;
     mc_runtime_stats_t total{}, since_reset{};
     uint64_t min_free = ~0ull;
+    StepGraph step_graph;
+    uint64_t graph_launches = 0;
 };
 
 struct GroupImpl {
@@ -121,6 +138,7 @@ struct GroupImpl {
     int32_t* h_tok = nullptr;  // pinned staging of the step's tokens
     hipEvent_t ev = nullptr;
     mc_kv_layout_t layout{};
+    StepGraph step_graph[kMaxSlots + 1];  // by the number of slots in the step
 };
 
 mc_status_t set_device(int id, const char* who) {
@@ -144,10 +162,39 @@ mc_status_t set_device(int id, const char* who) {
         if (_s != MC_OK) return _s;        \
     } while (0)
 
+// Runs `body` (launches on st): eagerly, or through a graph captured at the
+// first call and replayed afterwards.
+template <class F>
+mc_status_t run_step(bool use_graph, StepGraph& sg, hipStream_t st, F&& body) {
+    if (!use_graph) return body();
+    if (sg.exec == nullptr) {
+        HIP_OR_RETURN(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal),
+                      "decode step: hipStreamBeginCapture failed");
+        const mc_status_t bs = body();
+        hipGraph_t graph = nullptr;
+        const hipError_t e = hipStreamEndCapture(st, &graph);
+        if (bs != MC_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return bs;
+        }
+        if (e != hipSuccess) return check_hip(e, "decode step: hipStreamEndCapture failed");
+        const hipError_t e2 = hipGraphInstantiate(&sg.exec, graph, nullptr, nullptr, 0);
+        if (e2 != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            sg.exec = nullptr;
+            return check_hip(e2, "decode step: hipGraphInstantiate failed");
+        }
+        sg.graph = graph;
+    }
+    HIP_OR_RETURN(hipGraphLaunch(sg.exec, st), "decode step: hipGraphLaunch failed");
+    return MC_OK;
+}
+
 void release_session(SessionImpl* s) {
     if (s == nullptr) return;
     (void)hipSetDevice(s->model->device_id);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
+    destroy_graph(s->step_graph);
     if (s->kv) mc_kv_allocator_destroy(s->kv);
     if (s->arena) (void)hipFree(s->arena);
     if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -170,6 +217,7 @@ void release_group(GroupImpl* g) {
             g->members[i] = nullptr;
         }
     if (g->ev) (void)hipEventDestroy(g->ev);
+    for (auto& sg : g->step_graph) destroy_graph(sg);
     if (g->h_tables) (void)hipHostFree(g->h_tables);
     if (g->h_tok) (void)hipHostFree(g->h_tok);
     if (g->arena) (void)hipFree(g->arena);
@@ -282,6 +330,7 @@ mc_status_t mc_model_load(const char* model_dir, const mc_model_options_t* optio
     m->device_id = options->device_id;
     m->max_sessions = options->max_sessions;
     m->max_ctx = options->max_context_tokens;
+    m->use_graphs = options->enable_cuda_graph != 0u;
     m->total_vram = prop.totalGlobalMem;
     *out_model = mc_model{m};
     return MC_OK;
@@ -503,14 +552,18 @@ mc_status_t mc_decode_one(mc_session_t session, const mc_generation_config_t* co
     MC_OR_RETURN(mc_kv_allocator_ensure_pages_for(s->kv, s->seq_len + 1u, st));
     // Per layer: synthetic row of (d_next_token, seq_len), phase0 decode
     // attention at limit = seq_len (appends K/V of that position).
-    for (uint32_t l = 0; l < kLayers; ++l) {
-        MC_OR_RETURN(launch_synth_qkv(s->qkv, 1, &s->d_state->next_token,
-                                      &s->d_state->seq_len, l, st));
-        MC_OR_RETURN(mc_kv_attention_decode(s->qkv, &s->d_state->seq_len, l, s->d_pt,
-                                            s->pool, s->layout, s->partials, s->max_chunks,
-                                            s->attn_out, st, s->inv_freq, s->chunk_pos,
-                                            s->partials2));
-    }
+    MC_OR_RETURN(run_step(s->model->use_graphs, s->step_graph, st, [&]() -> mc_status_t {
+        for (uint32_t l = 0; l < kLayers; ++l) {
+            MC_OR_RETURN(launch_synth_qkv(s->qkv, 1, &s->d_state->next_token,
+                                          &s->d_state->seq_len, l, st));
+            MC_OR_RETURN(mc_kv_attention_decode(s->qkv, &s->d_state->seq_len, l, s->d_pt,
+                                                s->pool, s->layout, s->partials,
+                                                s->max_chunks, s->attn_out, st, s->inv_freq,
+                                                s->chunk_pos, s->partials2));
+        }
+        return MC_OK;
+    }));
+    if (s->model->use_graphs) s->graph_launches += 1;
     s->h_tok = mock_token(s->seq_len, s->rng);
     HIP_OR_RETURN(hipMemcpyAsync(&s->d_state->next_token, &s->h_tok, 4u,
                                  hipMemcpyHostToDevice, st),
@@ -547,7 +600,7 @@ mc_status_t mc_get_stats(mc_session_t session, mc_runtime_stats_t* out_stats) {
     if (fr < s->min_free) s->min_free = fr;
     *out_stats = s->total;
     out_stats->peak_vram_bytes = s->model->total_vram - s->min_free;
-    out_stats->cuda_graph_launches = 0;
+    out_stats->cuda_graph_launches = s->graph_launches;
     return MC_OK;
     MC_GUARD_END
 }
@@ -800,12 +853,17 @@ mc_status_t mc_batch_step(mc_batch_group_t group, const uint32_t* slot_ids, uint
                                  hipMemcpyHostToDevice, st),
                   "mc_batch_step: slot pointer table H2D failed");
     const mc_kv_layout_t lay = g->members[slot_ids[0]]->layout;
-    for (uint32_t l = 0; l < kLayers; ++l) {
-        MC_OR_RETURN(launch_synth_qkv_batch(g->qkv, n, g->d_tok, g->d_pos, l, st));
-        MC_OR_RETURN(mc_kv_attention_decode_batch(
-            g->qkv, g->d_pos, n, l, g->d_pt, g->d_kv, lay, g->partials, g->max_chunks,
-            g->out, st, g->inv_freq, g->chunk_pos, g->partials2));
-    }
+    MC_OR_RETURN(run_step(g->model->use_graphs, g->step_graph[n], st, [&]() -> mc_status_t {
+        for (uint32_t l = 0; l < kLayers; ++l) {
+            MC_OR_RETURN(launch_synth_qkv_batch(g->qkv, n, g->d_tok, g->d_pos, l, st));
+            MC_OR_RETURN(mc_kv_attention_decode_batch(
+                g->qkv, g->d_pos, n, l, g->d_pt, g->d_kv, lay, g->partials, g->max_chunks,
+                g->out, st, g->inv_freq, g->chunk_pos, g->partials2));
+        }
+        return MC_OK;
+    }));
+    if (g->model->use_graphs)
+        for (uint32_t i = 0; i < n; ++i) g->members[slot_ids[i]]->graph_launches += 1;
     for (uint32_t i = 0; i < n; ++i) {
         SessionImpl* s = g->members[slot_ids[i]];
         if (!s->rng_seeded) {

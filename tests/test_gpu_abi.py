@@ -257,3 +257,49 @@ def test_session_limit(rt, tmp_path):
     for s_ in (s2, s3):
         s_.close()
     m.close()
+
+
+def test_graph_mode_matches_eager(rt, tmp_path):
+    """enable_cuda_graph: the per-layer decode launches of a step (solo and
+    batched) are captured once into a HIP graph and replayed; tokens,
+    sequences and pool bytes equal the eager runtime's."""
+    rng = np.random.default_rng(3)
+    prompts = [[int(x) for x in rng.integers(0, 130560, n)] for n in (70, 257)]
+    res = []
+    for graphs in (0, 1):
+        m = rt.Model(str(tmp_path), rt.model_options(max_context_tokens=2048, max_sessions=4,
+                                                     enable_cuda_graph=graphs))
+        ss = [rt.Session(m) for _ in prompts]
+        for s_, p in zip(ss, prompts):
+            s_.prefill(p)
+        cfgs = [rt.gen_config(max_new_tokens=100, seed=5 + i) for i in range(2)]
+        toks = [[ss[0].decode_one(cfgs[0]) for _ in range(4)]]
+        g = rt.BatchGroup(m, 4, 2048)
+        slots = [g.add(s_) for s_ in ss]
+        toks += [g.step(slots, cfgs) for _ in range(3)]
+        toks += [g.step(slots[1:], cfgs[1:]) for _ in range(2)]
+        for sl in slots:
+            g.remove(sl)
+        toks.append([ss[1].decode_one(cfgs[1]) for _ in range(2)])
+        pools = []
+        for s_ in ss:
+            info = s_.info()
+            nb = info["pages_owned"] * P * 1024
+            lay = info["layout"]
+            pools.append([d2h(info["d_pool"] + l * lay.max_pages * P * 1024, nb, np.uint16)
+                          for l in (0, 41)])
+            pools.append(s_.seq(info["seq_len"]))
+        launches = [s_.stats().cuda_graph_launches for s_ in ss]
+        res.append((toks, pools, launches))
+        g.close()
+        for s_ in ss:
+            s_.close()
+        m.close()
+    (t0, p0, l0), (t1, p1, l1) = res
+    assert t0 == t1
+    for a, b in zip(p0, p1):
+        if isinstance(a, list) and a and isinstance(a[0], np.ndarray):
+            assert all(np.array_equal(x, y) for x, y in zip(a, b))
+        else:
+            assert a == b
+    assert l0 == [0, 0] and l1 == [4 + 3, 3 + 2 + 2]
