@@ -9,7 +9,7 @@ the headline workload C4 (one session, 131072 cached tokens in 2048 pages of
 second over the whole timed region (inputs resident in HBM); the other
 configurations are reported under "configs".
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,pf]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,c5,pf]
 """
 from __future__ import annotations
 
@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c4,c3,c1,c2,pf")
+    ap.add_argument("--configs", default="c4,c3,c1,c2,c5,pf")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (eager launches)")
@@ -132,7 +132,7 @@ def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
     inv = torch.empty(64, dtype=torch.float32, device=dev)
     kvm.launch_rope_inv_freq_init(inv, 5e6)
     parts = torch.empty(16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(16 * 32 * 130, dtype=torch.float32, device=dev)
     out = torch.empty(LAYERS * 2048, dtype=torch.int16, device=dev)
     def step_on(pool):
         def f():
@@ -190,7 +190,7 @@ def bench_decode_batch(kvm, torch, dev, timer, B, ctx, steps, warmup):
     inv = torch.empty(64, dtype=torch.float32, device=dev)
     kvm.launch_rope_inv_freq_init(inv, 5e6)
     parts = torch.empty(B * 16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.zeros(B * (16 * 32 * 130 + 2), dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(B * (16 * 32 * 130), dtype=torch.float32, device=dev)
     out = torch.empty(B * 2048, dtype=torch.int16, device=dev)
 
     def step_f():
@@ -210,6 +210,88 @@ def bench_decode_batch(kvm, torch, dev, timer, B, ctx, steps, warmup):
         "pct_hbm_peak": 100.0 * bytes_layer * LAYERS / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "tokens_per_s": B * 1e3 / ms,
         "algorithmic_bytes_per_layer": bytes_layer,
+    }
+
+
+def bench_churn(kvm, torch, dev, timer, steps=64, B=8, max_ctx=131072, seed=5):
+    """C5: B sessions with lengths log-uniform in [16, max_ctx) in one shared
+    pool; over `steps` batched decode steps sessions finish and new ones are
+    admitted (pages freed and reused through the shared pool allocator), every
+    step appends one token per session (phase0) and attends (ragged limits,
+    chunk tier of max_ctx). The 28-layer step is one captured graph; the
+    host-side churn (allocator, page-table uploads, limits) runs between
+    replays and is included in the step wall time."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    draw = lambda: int(min(max_ctx - steps - 1,
+                           round(np.exp(rng.uniform(np.log(16), np.log(max_ctx))))))
+    maxp = B * (max_ctx // P + 2)
+    lay = kvm.KvLayout(maxp, P, LAYERS)
+    C = kvm.attention_decode_chunk_pos(max_ctx)
+    NC = kvm.attention_decode_max_chunks(max_ctx, C)
+    pool = make_session_pool(torch, dev, maxp, LAYERS)
+    alloc = kvm.SharedPagePool(maxp, P, B)
+    d_tabs = [torch.zeros(maxp, dtype=torch.int32, device=dev) for _ in range(B)]
+    lens = [draw() for _ in range(B)]
+    for s in range(B):
+        alloc.ensure(s, lens[s], d_tabs[s])
+    lims = torch.zeros(B, dtype=torch.int32, device=dev)
+    h_lims = torch.zeros(B, dtype=torch.int32).pin_memory()
+    tab = lambda ptrs: torch.tensor(ptrs, dtype=torch.int64, device=dev)
+    d_pos = tab([lims.data_ptr() + 4 * s for s in range(B)])
+    d_pt = tab([t.data_ptr() for t in d_tabs])
+    d_kv = tab([pool.data_ptr()] * B)
+    qs = q_rows(torch, dev, LAYERS * B)
+    inv = torch.empty(64, dtype=torch.float32, device=dev)
+    kvm.launch_rope_inv_freq_init(inv, 5e6)
+    parts = torch.empty(B * 16 * NC * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.empty(B * 16 * 32 * 130, dtype=torch.float32, device=dev)
+    out = torch.empty(B * 2048, dtype=torch.int16, device=dev)
+
+    def step_f():
+        for l in range(LAYERS):
+            kvm.launch_attention_decode_batch(qs[l * B * 2560:], d_pos, B, l, d_pt, d_kv, lay,
+                                              parts, NC, out, d_inv_freq=inv, chunk_pos=C,
+                                              d_partials2=parts2)
+
+    def host_churn(first):
+        for s in range(B):
+            if not first and rng.random() < 0.1:  # finish -> admit a new session
+                alloc.release(s)
+                lens[s] = draw()
+            alloc.ensure(s, lens[s] + 1, d_tabs[s])
+            h_lims[s] = lens[s]
+        lims.copy_(h_lims, non_blocking=True)
+
+    host_churn(True)
+    step = timer.capture([step_f])
+    torch.cuda.synchronize()
+    kv_tokens = 0
+    gpu_ms = 0.0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    for it in range(steps):
+        if it:
+            host_churn(False)
+        kv_tokens += sum(l + 1 for l in lens)
+        e0.record()
+        step()
+        e1.record()
+        e1.synchronize()
+        gpu_ms += e0.elapsed_time(e1)
+        for s in range(B):
+            lens[s] += 1
+    wall = time.perf_counter() - t0
+    alloc.close()
+    kv_bytes = kv_tokens * KV_BYTES_PER_TOKEN * LAYERS
+    return {
+        "sessions": B, "steps": steps, "max_ctx": max_ctx, "chunk_pos": C,
+        "mean_ctx": kv_tokens / steps / B,
+        "gpu_us_per_layer": gpu_ms * 1e3 / steps / LAYERS,
+        "wall_ms_per_step": wall * 1e3 / steps,
+        "kv_gbs_gpu": kv_bytes / (gpu_ms * 1e-3) / 1e9,
+        "pct_hbm_peak_gpu": 100.0 * kv_bytes / (gpu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "tokens_per_s": B * steps / wall,
     }
 
 
@@ -357,6 +439,11 @@ def main():
         log(res["c2_append_8448"])
         torch.cuda.empty_cache()
 
+    if "c5" in cfgs:
+        log("C5: churn, 8 sessions, log-uniform lengths, 64 steps ...")
+        res["c5_churn"] = bench_churn(kvm, torch, dev, timer)
+        log(res["c5_churn"])
+        torch.cuda.empty_cache()
     if "pf" in cfgs:
         for base in (0, 8448):
             log(f"prefill attention 8448 tokens at base {base} ...")

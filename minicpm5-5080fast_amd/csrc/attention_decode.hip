@@ -685,10 +685,19 @@ __global__ void __launch_bounds__(128) merge_a_kernel(
     const uint32_t d = threadIdx.x;
     const float* P = partials + (((size_t)slot * kHq + qh) * NC + s) * kPartial;
     Loaded<NMAX> x;
-    load_partials<NMAX>(P, (size_t)kSplit2 * kPartial, (NC - s + kSplit2 - 1u) / kSplit2, x);
-    const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
-    const uint32_t nv = n_valid_chunks(limit, C, NC);
-    const uint32_t n = s < nv ? (nv - s + kSplit2 - 1u) / kSplit2 : 0u;
+    uint32_t nv, n;
+    if constexpr (BATCH) {
+        // Ragged slots: read the limit first and load only the valid chunks
+        // (a short slot would otherwise pull its whole stale buffer).
+        nv = n_valid_chunks(*slot_pos[slot], C, NC);
+        n = s < nv ? (nv - s + kSplit2 - 1u) / kSplit2 : 0u;
+        load_partials<NMAX>(P, (size_t)kSplit2 * kPartial, n > 0u ? n : 1u, x);
+    } else {
+        load_partials<NMAX>(P, (size_t)kSplit2 * kPartial, (NC - s + kSplit2 - 1u) / kSplit2,
+                            x);
+        nv = n_valid_chunks(*d_pos, C, NC);
+        n = s < nv ? (nv - s + kSplit2 - 1u) / kSplit2 : 0u;
+    }
     float M, L;
     const float A = fold_loaded<NMAX>(x, n, M, L);
     float* pw2 = partials2 + (((size_t)slot * kHq + qh) * kSplit2 + s) * kPartial;
@@ -709,10 +718,15 @@ __global__ void __launch_bounds__(128) merge_b_kernel(
     uint16_t* __restrict__ out) {
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
     Loaded<kSplit2> x;
-    load_partials<kSplit2>(partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial,
-                           kPartial, kSplit2, x);
-    const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
-    const bool active = n_valid_chunks(limit, C, NC) > 1u;
+    const float* base = partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial;
+    bool active;
+    if constexpr (BATCH) {
+        active = n_valid_chunks(*slot_pos[slot], C, NC) > 1u;
+        load_partials<kSplit2>(base, kPartial, active ? kSplit2 : 1u, x);
+    } else {
+        load_partials<kSplit2>(base, kPartial, kSplit2, x);
+        active = n_valid_chunks(*d_pos, C, NC) > 1u;
+    }
     float M, L;
     const float A = fold_loaded<kSplit2>(x, kSplit2, M, L);
     if (active)
@@ -734,9 +748,14 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
     bool active;
     if constexpr (NMAX > 0u) {
         Loaded<NMAX> x;
-        load_partials<NMAX>(base, kPartial, NC, x);
-        const uint32_t limit = BATCH ? *slot_pos[slot] : *d_pos;
-        const uint32_t nv = n_valid_chunks(limit, C, NC);
+        uint32_t nv;
+        if constexpr (BATCH) {
+            nv = n_valid_chunks(*slot_pos[slot], C, NC);
+            load_partials<NMAX>(base, kPartial, nv, x);
+        } else {
+            load_partials<NMAX>(base, kPartial, NC, x);
+            nv = n_valid_chunks(*d_pos, C, NC);
+        }
         active = nv > 1u;
         A = fold_loaded<NMAX>(x, nv, M, L);
     } else {
@@ -751,15 +770,17 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
 }
 
 // Chunks per workgroup: enough workgroups for ~kTargetBlocks resident blocks
-// (2 per CU on 256 CUs) when there are more chunks than that; C % 64 == 0 is
-// needed for cpw > 1 (all 4 waves then cross chunk boundaries together).
+// (2 per CU on 256 CUs) for ONE session whose context fills all NC chunks.
+// The slot count is deliberately left out: batched limits are ragged and read
+// on the device, and sizing for B full sessions would give a long session a
+// few very long workgroups. C % 64 == 0 is needed for cpw > 1 (all 4 waves
+// then cross chunk boundaries together).
 #ifndef MCKV_TARGET_BLOCKS
 #define MCKV_TARGET_BLOCKS 512
 #endif
-uint32_t chunks_per_block(uint32_t NC, uint32_t B, uint32_t C) {
+uint32_t chunks_per_block(uint32_t NC, uint32_t C) {
     if (C % 64u != 0u) return 1u;
-    const uint32_t units = NC * kHkv * B;
-    const uint32_t cpw = units / MCKV_TARGET_BLOCKS;
+    const uint32_t cpw = NC * kHkv / MCKV_TARGET_BLOCKS;
     return cpw < 1u ? 1u : cpw;
 }
 
@@ -770,7 +791,7 @@ mc_status_t launch_chunks(const uint16_t* q, const uint32_t* d_pos,
                           uint16_t* pool, uint16_t* const* slot_kv, DevLayout ly,
                           float* partials, uint32_t NC, uint16_t* out,
                           hipStream_t st, const float* inv_freq, uint32_t C) {
-    const uint32_t cpw = chunks_per_block(NC, B, C);
+    const uint32_t cpw = chunks_per_block(NC, C);
     const dim3 grid((NC + cpw - 1u) / cpw, kHkv, B);
 #define MCKV_LAUNCH_CHUNK(PH, PG, TP)                                                      \
     hipLaunchKernelGGL((decode_chunk_kernel<PH, BATCH, PG, TP>), grid, dim3(kThreads), 0, st, \

@@ -75,7 +75,7 @@ def test_churn_batched_decode(kvm, orc, dev):
     tab = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
     t_lims, t_pts, t_kv = tab(d_lims), tab(d_tabs), tab([pool_d] * B)
     parts = torch.zeros(B * 16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.zeros(B * (16 * 32 * 130 + 2), dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(B * (16 * 32 * 130), dtype=torch.float32, device=dev)
     out = torch.zeros(B * 2048, dtype=torch.int16, device=dev)
     freed, reused = set(), 0
     for step in range(STEPS):

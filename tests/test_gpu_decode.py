@@ -41,7 +41,7 @@ def run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, limit, C, NC, two_level
     d_pt = to_dev(np.asarray(pt, dtype=np.uint32), dev)
     d_pos = to_dev(np.array([limit], dtype=np.uint32), dev)
     parts = torch.full((16 * NC * 130,), float("nan"), dtype=torch.float32, device=dev)
-    parts2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(16 * 32 * 130, dtype=torch.float32, device=dev)
     out = torch.zeros(2048, dtype=torch.int16, device=dev)
     kvm.launch_attention_decode(d_q, d_pos, layer, d_pt, d_pool, lay, parts, NC, out,
                                 d_inv_freq=inv, chunk_pos=C,
@@ -204,7 +204,7 @@ def test_phase0_matches_rope_then_attend(kvm, orc, dev, limit):
     d_pos = to_dev(np.array([limit], dtype=np.uint32), dev)
     kvm.launch_rope_kv(d_qkv_a, 1, d_pos, layer, d_pt, d_pool_a, lay, 5e6, d_inv_freq=inv)
     pa = torch.empty(16 * NC * 130, dtype=torch.float32, device=dev)
-    p2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
+    p2 = torch.zeros(16 * 32 * 130, dtype=torch.float32, device=dev)
     out_a = torch.zeros(2048, dtype=torch.int16, device=dev)
     kvm.launch_attention_decode(d_qkv_a, d_pos, layer, d_pt, d_pool_a, lay, pa, NC, out_a,
                                 chunk_pos=64, d_partials2=p2)
@@ -255,7 +255,7 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed):
     tab = lambda ts: torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64,
                                   device=dev)
     parts = torch.zeros(B * 16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.zeros(B * (16 * 32 * 130 + 2), dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(B * (16 * 32 * 130), dtype=torch.float32, device=dev)
     out = torch.zeros(B * 2048, dtype=torch.int16, device=dev)
     kvm.launch_attention_decode_batch(d_q, tab(d_lims), B, layer, tab(d_pts),
                                       tab([d_pool] * B), lay, parts, NC, out, d_inv_freq=inv,
@@ -271,7 +271,7 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed):
         o1 = torch.zeros(2048, dtype=torch.int16, device=dev)
         kvm.launch_attention_decode(to_dev(q[s], dev), d_lims[s], layer, d_pts[s], d_pool1,
                                     lay, p1, NC, o1, d_inv_freq=inv, chunk_pos=C,
-                                    d_partials2=torch.zeros(16 * 32 * 130 + 2,
+                                    d_partials2=torch.zeros(16 * 32 * 130,
                                                             dtype=torch.float32, device=dev))
         torch.cuda.synchronize()
         singles.append(from_dev(o1))
@@ -351,7 +351,7 @@ def test_repeat_launch_and_graph_replay(kvm, orc, dev, ctx, C):
     NC = -(-(ctx + 8) // C)
     d_pool, d_q, d_pt = to_dev(pool, dev), to_dev(q, dev), to_dev(pt, dev)
     parts = torch.zeros(16 * NC * 130, dtype=torch.float32, device=dev)
-    parts2 = torch.zeros(16 * 32 * 130 + 2, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(16 * 32 * 130, dtype=torch.float32, device=dev)
     d_pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
 
     def run(out):
