@@ -673,9 +673,9 @@ __device__ __forceinline__ float fold_loaded(const Loaded<NMAX>& x, uint32_t n, 
 }
 
 // Level-1 -> level-2 merge. grid = (B*16, 32), block = 128 (thread = dim).
-// NMAX >= ceil(NC / 32). The partial loads are issued before the limit is
-// read; no block returns early (stores are predicated), so the compiler
-// cannot sink the loads behind the limit.
+// NMAX >= ceil(NC / 32). Single session: the partial loads are issued before
+// the limit is read; no block returns early (stores are predicated), so the
+// compiler cannot sink the loads behind the limit.
 template <bool BATCH, uint32_t NMAX>
 __global__ void __launch_bounds__(128) merge_a_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
