@@ -79,6 +79,12 @@ constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 #ifndef MCKV_RING
 #define MCKV_RING 2
 #endif
+#ifndef MCKV_ROW_LOADS
+// Whole-row loads + LDS transpose for the 64-position chunk tier (TPW == 1):
+// measured faster there (2K contexts), slower at C = 256 (128K), where the
+// operand-layout loads spaced by the per-tile compute stream better.
+#define MCKV_ROW_LOADS 1
+#endif
 #ifndef MCKV_NT_LOADS
 #define MCKV_NT_LOADS 0
 #endif
@@ -138,6 +144,9 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     __shared__ float s_cs[64], s_sn[64];
     __shared__ __align__(16) uint16_t s_fresh[256];  // phase0: K | V of `limit`
     __shared__ uint32_t s_pages[kPageCache];         // page ids of this block's range
+    constexpr bool ROWS = MCKV_ROW_LOADS && TPW == 1u;
+    // per wave: K and V tile, 16 x 256 B (row loads only)
+    __shared__ uint4 s_x[ROWS ? kWaves : 1u][ROWS ? 2u * 16u * 16u : 1u];
     __shared__ float s_m[kFoldSlots][kWaves][kGroup], s_l[kFoldSlots][kWaves][kGroup];
     __shared__ __align__(16) float s_acc[kFoldSlots][kWaves][kGroup][kD];
 
@@ -183,6 +192,29 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // do not wait for the staging barrier.
     auto load_tile = [&](Tile& T, uint32_t c, uint32_t j, bool direct) {
         const uint32_t t0 = c * C + j * kTile;
+        if constexpr (ROWS) {
+            // Row loads: lane (q = lane/16, x = lane%16) reads the 16-byte chunk x
+            // of the K and V head rows of tokens t0 + q + 4r (r < 4), so every 16
+            // lanes read one whole 256-byte head row (whole 128-byte lines per
+            // request). xpose() restores the MFMA operand layout through LDS.
+            const uint32_t cend = chunk_end(c);
+            uint32_t page_u = 0;
+            if (PAGE16 && cached_pages && !direct)
+                page_u = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
+            else if constexpr (PAGE16)
+                page_u = ((const __attribute__((address_space(4))) uint32_t*)(pt))
+                    [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t p = min(t0 + grp + 4u * r, cend);
+                const uint32_t page = PAGE16 ? page_u : pt[p >> ly.log2p];
+                const uint16_t* src =
+                    pool + token_base(ly, layer, page, p & ly.pmask) + kvh * kD + 8u * tok;
+                T.k[r] = ld16(src);
+                T.v[r] = ld16(src + 256u);
+            }
+            return;
+        }
         const uint32_t p = min(t0 + tok, chunk_end(c));
         uint32_t page;
         if (PAGE16 && cached_pages && !direct)
@@ -198,6 +230,32 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             T.k[m] = ld16(src + 32u * m);
             T.v[m] = ld16(src + 256u + 32u * m);
         }
+    };
+    // Row-loaded tile -> operand layout (lane (row, group) holds dims
+    // [32m + 8*group, +8) of token row, m < 4) through this wave's LDS tile:
+    // chunk x of token t is stored at slot x ^ t of row t, so both the stores
+    // (16 chunks of 4 rows per instruction) and the operand reads (one chunk
+    // of 16 rows per lane group) spread over all LDS banks. A wave reads only
+    // what it wrote, in order: no barrier is needed.
+    auto xpose = [&](const Tile& T) -> Tile {
+        if constexpr (!ROWS) return T;
+        uint4* xs = s_x[wave];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t t = grp + 4u * r;
+            xs[t * 16u + (tok ^ t)] = T.k[r];
+            xs[256u + t * 16u + (tok ^ t)] = T.v[r];
+        }
+        __builtin_amdgcn_wave_barrier();
+        Tile O;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t x = (4u * m + grp) ^ tok;
+            O.k[m] = xs[tok * 16u + x];
+            O.v[m] = xs[256u + tok * 16u + x];
+        }
+        __builtin_amdgcn_wave_barrier();
+        return O;
     };
     // Next (chunk, tile) of this wave after (c, j); false past the range.
     auto advance = [&](uint32_t& c, uint32_t& j) {
@@ -481,7 +539,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 
     auto process = [&](const Tile& T, uint32_t c, uint32_t j) {
         while (cc < c) fold();
-        accumulate(T, c * C + j * kTile, chunk_end(c));
+        accumulate(xpose(T), c * C + j * kTile, chunk_end(c));
     };
 
     if constexpr (TPW > 0) {
@@ -509,7 +567,8 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                     const uint32_t j = wave + 4u * i;
                     if (cc2 < c_end && j < chunk_tiles(cc2)) {
                         while (cc < cc2) fold();
-                        accumulate(R[g % RING], cc2 * C + j * kTile, chunk_end(cc2));
+                        accumulate(xpose(R[g % RING]), cc2 * C + j * kTile,
+                                   chunk_end(cc2));
                     }
                 }
             }

@@ -142,6 +142,41 @@ def test_decode_chunk_tiers(kvm, orc, dev, C, P):
     check_vs_ref(orc, got, ref, f"tier C={C} P={P}")
 
 
+@pytest.mark.parametrize("C", [64, 128, 48])
+@pytest.mark.parametrize("P", [1, 4, 8])
+@pytest.mark.parametrize("ph0", [False, True])
+def test_decode_small_pages(kvm, orc, dev, C, P, ph0):
+    """Pages smaller than a 16-position tile: page ids looked up per position
+    (both tile-load layouts: C = 64 uses whole-row loads, C = 128 operand-
+    layout loads, C = 48 the generic schedule)."""
+    import torch
+    rng = np.random.default_rng(C * 31 + P + ph0)
+    ctx = 777
+    maxp = -(-ctx // P) + 3
+    pt = rng.permutation(maxp)[: -(-ctx // P)].astype(np.uint32)
+    L, layer = 2, 1
+    pool = np.full(maxp * P * 512 * L, POISON, dtype=np.uint16)
+    n_fill = ctx - 1 if ph0 else ctx
+    for j in range(n_fill):
+        base = orc.kv_off(P, maxp, layer, int(pt[j // P]), j % P, 0, 0, 0)
+        pool[base:base + 512] = randn_bf16(rng, 512, 0.5)
+    q = randn_bf16(rng, 2560, 1.0)
+    NC = -(-1024 // C)
+    limit = ctx - 1
+    inv = None
+    if ph0:
+        inv = torch.empty(64, dtype=torch.float32, device=dev)
+        kvm.launch_rope_inv_freq_init(inv, 5e6)
+    got, _, pool_after = run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, limit, C, NC,
+                                    inv=inv)
+    qkv_o, pool_o = q.reshape(1, 2560).copy(), pool.copy()
+    if ph0:
+        orc.rope_append(qkv_o, 1, limit, layer, pt, P, maxp, 5e6, 1, pool_o)
+        assert np.array_equal(pool_after, pool_o)
+    ref = orc.attn_ref(qkv_o, 1, limit, layer, pool_o, pt, P, maxp)[0]
+    check_vs_ref(orc, got, ref, f"small pages C={C} P={P} ph0={ph0}")
+
+
 @pytest.mark.parametrize("N,limit", [(257, 257 * 64 - 1), (257, 5 * 64 + 10),
                                      (512, 512 * 64 - 1), (512, 33 * 64),
                                      (2048, 2048 * 64 - 1), (2048, 700 * 64 + 3)])
