@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X paged KV-cache hot path.
 
-Metric (BASELINE.json): decode-attention us/layer and KV HBM GB/s (% of peak) at
+Metric: decode-attention us/layer and KV HBM GB/s (% of peak) at
 2K, 8x2K batch and 128K. One "step" = one decode step of the 28-layer stack at
 the headline workload C4 (one session, 131072 cached tokens in 2048 pages of
 64, chunk 256, two-level merge): per layer the fused append+attend decode

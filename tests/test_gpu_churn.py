@@ -1,4 +1,4 @@
-"""Mixed-length churn (BASELINE config 5) on the GPU: 8 sessions with lengths
+"""Mixed-length churn on the GPU: 8 sessions with lengths
 log-uniform in [16, 131072) share one pool; over 64 batched decode steps
 sessions finish and new ones are admitted (their pages freed and reused), and
 every step appends one token per session (phase0) and attends it with the
