@@ -367,6 +367,43 @@ def bench_prefill(kvm, torch, dev, timer, T, base, steps, warmup):
     }
 
 
+def host_threads() -> int:
+    """CPU threads for the host baselines: the cores this process may run on,
+    capped at the 16-core share a one-GPU box gives a job."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_append_baseline(seconds: float):
+    """The oracle's kernel-exact RoPE append (oracle/kv_oracle.c
+    orc_rope_append, one thread) over one 8448-token chunk of one layer,
+    repeated for about `seconds`; same bytes as the GPU C2 line."""
+    import numpy as np
+    import oracle
+    T = 8448
+    maxp = T // P
+    rng = np.random.default_rng(1)
+    qkv0 = oracle.f32_to_bf16(rng.standard_normal(T * 2560, dtype=np.float32)).reshape(T, 2560)
+    pt = rng.permutation(maxp).astype(np.uint32)
+    pool = np.zeros(maxp * P * 512, dtype=np.uint16)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        qkv = qkv0.copy()
+        oracle.rope_append(qkv, T, 0, 0, pt, P, maxp, 1e4, 1, pool)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    per_chunk = dt / n
+    all_bytes = T * 2560 * 2 * 2  # row read + q / K / V written
+    return {"tokens_per_s": T / per_chunk, "gbs": all_bytes / per_chunk / 1e9,
+            "cores": 1, "kind": "port",
+            "sample": f"{n} x 8448-token append of one layer, {per_chunk * 1e3:.1f} ms each"}
+
+
 def cpu_baseline(seconds: float):
     """The oracle's fp32 decode (oracle/kv_oracle.c orc_decode_cpu_mt) on host
     cores: one layer of the C4 workload (131072 tokens) per call, repeated for
@@ -375,7 +412,7 @@ def cpu_baseline(seconds: float):
     import oracle
     ctx = 131072
     maxp = ctx // P
-    threads = os.cpu_count() or 1
+    threads = host_threads()
     rng = np.random.default_rng(0)
     pool = oracle.f32_to_bf16(rng.standard_normal(maxp * P * 512, dtype=np.float32)
                               / np.float32(128 ** 0.5))
@@ -462,6 +499,8 @@ def main():
 
     head = res.get("c4_128k")
     cpu = None if args.no_cpu or head is None else cpu_baseline(args.cpu_seconds)
+    if not args.no_cpu and "c2_append_8448" in res:
+        res["cpu_append_8448"] = cpu_append_baseline(min(3.0, args.cpu_seconds))
     line = {
         "metric": "decode-attn us/layer & KV HBM GB/s (% peak) at 2K, 8x2K batch, 128K",
         "value": round(head["kv_gbs"], 2) if head else None,
