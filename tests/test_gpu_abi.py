@@ -303,3 +303,36 @@ def test_graph_mode_matches_eager(rt, tmp_path):
         else:
             assert a == b
     assert l0 == [0, 0] and l1 == [4 + 3, 3 + 2 + 2]
+
+
+def test_long_prefill_multichunk(rt, tmp_path, orc):
+    """A 20000-token prompt (three prefill chunks of up to 8448 tokens) in a
+    131072-token session: K/V at chunk boundaries equal the kernel-exact
+    oracle, then decode steps (512-chunk tier, two-level merge) follow the
+    mock token rule."""
+    m = rt.Model(str(tmp_path), rt.model_options(max_context_tokens=131072, max_sessions=1))
+    s = rt.Session(m)
+    rng = np.random.default_rng(17)
+    prompt = [int(x) for x in rng.integers(0, 130560, 20000)]
+    s.prefill(prompt)
+    info = s.info()
+    assert info["seq_len"] == 20000 and info["pages_owned"] == -(-20000 // P)
+    lay = info["layout"]
+    pt = d2h(info["d_page_table"], 4 * info["pages_owned"], np.uint32)
+    assert pt.tolist() == list(range(info["pages_owned"]))
+    for layer in (0, 41):
+        for pos in (8447, 8448, 16895, 16896, 19999):
+            row = synth_row(orc, prompt[pos], pos, layer).reshape(1, 2560)
+            ref = np.zeros(lay.max_pages * P * 512 * L, np.uint16)
+            orc.rope_append(row, 1, pos, layer, pt, P, lay.max_pages, THETA, 1, ref)
+            off = orc.kv_off(P, lay.max_pages, layer, int(pt[pos // P]), pos % P, 0, 0, 0)
+            assert np.array_equal(pool_token(info, layer, pos, pt), ref[off:off + 512]), pos
+    cfg = rt.gen_config(max_new_tokens=8, seed=99)
+    rng_state = 99
+    for i in range(3):
+        want = mock_token(20000 + i, rng_state)
+        rng_state = xorshift32(rng_state)
+        assert s.decode_one(cfg) == want
+    assert s.info()["seq_len"] == 20003
+    s.close()
+    m.close()
