@@ -18,19 +18,20 @@
 // MI355X design: one 512-thread workgroup (8 wave64, 2 per SIMD) per (kv
 // head, 32-row q tile, key split); heavy (late) q tiles are launched first.
 // The 32 rows x 8 query heads of a KV head are 256 query vectors: wave w owns
-// two 16-column groups, group g holding rows 4w + 2g + {0, 1} x heads 0..7. Keys stream in
-// 32-position steps gathered through the page table into LDS (double
-// buffered, register-staged prefetch of the next step): K row-major, V
-// transposed (dims x keys) so that both MFMA operands are contiguous LDS
-// reads. Per step and column group:
-//   * S^T = K x Q^T: 2 key blocks x 4 v_mfma_f32_16x16x32_bf16 (Q^T in
+// two 16-column groups, group g holding rows 4w + 2g + {0, 1} x heads 0..7.
+// Keys stream in 64-position steps gathered through the page table into LDS
+// (three buffers, register-staged prefetch of the next step, page ids one
+// step ahead), K and V row-major. Per step and column group:
+//   * S^T = K x Q^T: 4 key blocks x 4 v_mfma_f32_16x16x32_bf16 (Q^T in
 //     registers for the whole kernel);
-//   * online softmax per column over the 32 keys (lane holds 8 scores, two
-//     cross-lane xor steps), p fp32 for l, bf16 for P.V;
-//   * O^T += V^T x P^T: 8 v_mfma_f32_16x16x32_bf16 over the 32 keys, with
-//     the contraction index permuted identically on both operands so that
-//     P^T is exactly the lanes' softmax output.
-// The online-softmax update runs per 32 keys (the reference updates per 16)
+//   * online softmax per column over the 64 keys (lane holds 16 scores, two
+//     cross-lane xor steps), exp2 with the scale folded into one FMA, p fp32
+//     for l, bf16 (v_cvt_pk_bf16_f32) for P.V;
+//   * O^T += V^T x P^T: 2 halves x 8 v_mfma_f32_16x16x32_bf16, V^T read from
+//     the row-major tile with gfx950's transposing LDS read, the contraction
+//     index permuted identically on both operands so that P^T is exactly the
+//     lanes' softmax output.
+// The online-softmax update runs per 64 keys (the reference updates per 16)
 // with a lazily moved reference max; both are exact restatements of softmax
 // and differ only in rounding.
 #include <hip/hip_runtime.h>
@@ -61,7 +62,7 @@ constexpr int kNKB = kStep / 16;     // 16-key blocks per step
 constexpr int kNH = kStep / 32;      // 32-key halves per step (one PV MFMA each)
 static_assert(kStep == 32 || kStep == 64, "step of 32 or 64 keys");
 constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
-constexpr uint32_t kVPitch = kStep + 4;  // sVt row pitch (bf16): keys + 4
+constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (conflict-free tr reads)
 constexpr uint32_t kBufs = 3;            // LDS K/V buffers (see the ping-pong)
 
 template <bool PAGE_STEP>
@@ -71,7 +72,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
     uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S) {
     __shared__ __align__(16) uint16_t sK[kBufs][kStep * kKPitch];
-    __shared__ __align__(16) uint16_t sVt[kBufs][kD * kVPitch];
+    __shared__ __align__(16) uint16_t sV[kBufs][kStep * kVPitch];
 
     const uint32_t ntq = (T + kQRows - 1u) / kQRows;
     const uint32_t s = blockIdx.x % S;
@@ -119,12 +120,10 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         for (int db = 0; db < 8; ++db) acc[g][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // Cooperative gather, 2 chunks of 16 bytes per thread: the K chunk of key
-    // tid/16, dims 8*(tid%16), and the V chunk of key tid%32, dims 8*(tid/32)
-    // (so that the transposed LDS stores of a wave hit consecutive keys of one
-    // dim row).
+    // Cooperative gather: per 32-key half, thread tid moves the 16-byte K and
+    // V chunks of key tid/16, dims 8*(tid%16) (16 threads per 256-byte row).
     uint4 stage[2 * kNH];  // [K chunks of each half, then V chunks]
-    const uint32_t kkey = tid >> 4, kdb = tid & 15u, vkey = tid & 31u, vdb = tid >> 5;
+    const uint32_t kkey = tid >> 4, kdb = tid & 15u;
     // Page ids are fetched one step ahead of the K/V loads that use them, so
     // a gather waits for one memory latency, not two. With P >= kStep a step lies
     // in one page and its id is read through the scalar path.
@@ -140,7 +139,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         } else {
 #pragma unroll
             for (int r = 0; r < 2 * kNH; ++r) {
-                const uint32_t pos = js * kStep + 32u * (r % kNH) + (r >= kNH ? vkey : kkey);
+                const uint32_t pos = js * kStep + 32u * (r % kNH) + kkey;
                 pg[r] = pos <= key_end ? pt[pos >> ly.log2p] : 0u;
             }
         }
@@ -149,8 +148,8 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
 #pragma unroll
         for (int r = 0; r < 2 * kNH; ++r) {
             const bool isv = r >= kNH;
-            const uint32_t key = 32u * (r % kNH) + (isv ? vkey : kkey);
-            const uint32_t dblk = isv ? vdb : kdb;
+            const uint32_t key = 32u * (r % kNH) + kkey;
+            const uint32_t dblk = kdb;
             const uint32_t pos = js * kStep + key;
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
 #ifdef PF_NO_GATHER
@@ -169,10 +168,8 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
 #pragma unroll
         for (int h = 0; h < kNH; ++h) {
             *reinterpret_cast<uint4*>(&sK[b][(32u * h + kkey) * kKPitch + kdb * 8u]) = stage[h];
-            const uint16_t* e = reinterpret_cast<const uint16_t*>(&stage[kNH + h]);
-            uint16_t* dst = &sVt[b][vdb * 8u * kVPitch + 32u * h + vkey];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) dst[i * kVPitch] = e[i];
+            *reinterpret_cast<uint4*>(&sV[b][(32u * h + kkey) * kVPitch + kdb * 8u]) =
+                stage[kNH + h];
         }
     };
 
@@ -195,17 +192,26 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     const bool late_pv = wave >= 4u;
     bf16x8 pb_prev[G][kNH];
     int bprev = 0;
-    auto pv = [&](const uint16_t* Vt, const bf16x8 (&pbv)[G][kNH]) {
-        // O^T += V^T x P^T per 32-key half h; contraction index i of lane
-        // group grp <-> key 32h + 16*(i/4) + 4*grp + i%4 on both operands.
+    // V^T operand straight from the row-major V tile with the transposing LDS
+    // read: within each 16-lane group, ds_read_b64_tr_b16 gives lane x the
+    // element x%4 of the 8-byte rows addressed by lanes 4j + x/4 (j < 4). With
+    // lane (4j + r) of group grp addressing key 4*grp + j, dims 16*db + 4r,
+    // lane x receives dim 16*db + x of keys 4*grp + j: the A operand of
+    // O^T += V^T x P^T. Contraction index i of lane group grp <-> key
+    // 32h + 16*(i/4) + 4*grp + i%4 on both operands.
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    const uint32_t tr_row = 4u * grp + (col >> 2), tr_col = 4u * (col & 3u);
+    auto pv = [&](const uint16_t* Vs, const bf16x8 (&pbv)[G][kNH]) {
 #pragma unroll
         for (int h = 0; h < kNH; ++h)
 #pragma unroll
             for (int db = 0; db < 8; ++db) {
-                const uint16_t* vr = Vt + (16u * db + col) * kVPitch + 32u * h + 4u * grp;
-                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16u);
-                const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                const uint16_t* vr = Vs + (32u * h + tr_row) * kVPitch + 16u * db + tr_col;
+                const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (__attribute__((address_space(3))) bf16x4*)(vr));
+                const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (__attribute__((address_space(3))) bf16x4*)(vr + 16u * kVPitch));
+                const bf16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int g = 0; g < G; ++g)
                     acc[g][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pbv[g][h],
@@ -221,8 +227,8 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
             if (js + 1u < js1) page_ids(js + 2u, pgn);
         }
         const uint16_t* K = sK[b];
-        const uint16_t* Vt = sVt[b];
-        if (late_pv && js > js0) pv(sVt[bprev], pb_prev);
+        const uint16_t* Vt = sV[b];
+        if (late_pv && js > js0) pv(sV[bprev], pb_prev);
 #ifdef PF_NO_COMPUTE
         if (K[tid] == 0x1234u) l_run[0] += 1.f;
         continue;
@@ -308,7 +314,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
             pv(Vt, pb);
         }
     }
-    if (late_pv && js0 <= js1) pv(sVt[bprev], pb_prev);
+    if (late_pv && js0 <= js1) pv(sV[bprev], pb_prev);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         l_run[g] += __shfl_xor(l_run[g], 16);
