@@ -248,11 +248,25 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         }
         __builtin_amdgcn_wave_barrier();
         Tile O;
+        // V^T operands with the transposing LDS read: within each 16-lane
+        // group, ds_read_b64_tr_b16 gives lane x the element x%4 of the 8-byte
+        // rows addressed by lanes 4j + x/4 (j < 4). Lane 4j + a of group grp
+        // addresses token 4*grp + j, dims 32m + 8a + 4h, so lane x receives
+        // dim 32m + 8(x/4) + 4h + x%4 of tokens 4*grp + j: the A operand of
+        // O^T += V^T x P^T with the same dim order the accumulator uses.
+        const uint32_t vt_tok = 4u * grp + (tok >> 2);
+        const uint16_t* vs = reinterpret_cast<const uint16_t*>(xs + 256u) + vt_tok * 128u;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const uint32_t x = (4u * m + grp) ^ tok;
             O.k[m] = xs[tok * 16u + x];
-            O.v[m] = xs[256u + tok * 16u + x];
+            const uint16_t* vr = vs + (((4u * m + (tok & 3u)) ^ vt_tok) * 8u);
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(vr));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(vr + 4));
+            const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+            O.v[m] = make_uint4(l2.x, l2.y, h2.x, h2.y);
         }
         __builtin_amdgcn_wave_barrier();
         return O;
@@ -454,12 +468,17 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                const f32x4 vt = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-                    half_s16x4(T.v[m], h), ident, z, 0, 0, 0);
+                s16x4 vop;
+                if constexpr (ROWS) {  // T.v already holds the V^T operands
+                    vop = half_s16x4(T.v[m], h);
+                } else {
+                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    vop = trunc_bf16x4(__builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        half_s16x4(T.v[m], h), ident, z, 0, 0, 0));
+                }
                 acc[m][h] = acc[m][h] * renew;
-                acc[m][h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(trunc_bf16x4(vt), pb,
-                                                                      acc[m][h], 0, 0, 0);
+                acc[m][h] =
+                    __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop, pb, acc[m][h], 0, 0, 0);
             }
     };
     // Chunk completion. Each wave stashes its state of chunk cc into an LDS
@@ -515,7 +534,18 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 F.k[m] = *reinterpret_cast<const uint4*>(&s_fresh[32u * m + 8u * grp]);
-                F.v[m] = *reinterpret_cast<const uint4*>(&s_fresh[128u + 32u * m + 8u * grp]);
+                if constexpr (ROWS) {  // V^T operand: dim d of the token in every k slot
+                    uint32_t w[2];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t d = 32u * m + 8u * (tok >> 2) + 4u * h + (tok & 3u);
+                        w[h] = (uint32_t)s_fresh[128u + d] * 0x10001u;
+                    }
+                    F.v[m] = make_uint4(w[0], w[0], w[1], w[1]);
+                } else {
+                    F.v[m] =
+                        *reinterpret_cast<const uint4*>(&s_fresh[128u + 32u * m + 8u * grp]);
+                }
             }
             accumulate(F, limit, limit);
         }
