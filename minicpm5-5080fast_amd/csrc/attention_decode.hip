@@ -85,6 +85,9 @@ constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 // operand-layout loads spaced by the per-tile compute stream better.
 #define MCKV_ROW_LOADS 1
 #endif
+#ifndef MCKV_V_ROW_LOADS
+#define MCKV_V_ROW_LOADS 1  // V row loads (+ transposing LDS reads) also for C > 64
+#endif
 #ifndef MCKV_NT_LOADS
 #define MCKV_NT_LOADS 0
 #endif
@@ -144,9 +147,10 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     __shared__ float s_cs[64], s_sn[64];
     __shared__ __align__(16) uint16_t s_fresh[256];  // phase0: K | V of `limit`
     __shared__ uint32_t s_pages[kPageCache];         // page ids of this block's range
-    constexpr bool ROWS = MCKV_ROW_LOADS && TPW == 1u;
+    constexpr bool ROWS = MCKV_ROW_LOADS && TPW == 1u;             // K and V row loads
+    constexpr bool VROWS = ROWS || (MCKV_V_ROW_LOADS && TPW > 1u);  // V row loads
     // per wave: K and V tile, 16 x 256 B (row loads only)
-    __shared__ uint4 s_x[ROWS ? kWaves : 1u][ROWS ? 2u * 16u * 16u : 1u];
+    __shared__ uint4 s_x[VROWS ? kWaves : 1u][VROWS ? 2u * 16u * 16u : 1u];
     __shared__ float s_m[kFoldSlots][kWaves][kGroup], s_l[kFoldSlots][kWaves][kGroup];
     __shared__ __align__(16) float s_acc[kFoldSlots][kWaves][kGroup][kD];
 
@@ -225,10 +229,23 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         else
             page = pt[p >> ly.log2p];
         const uint16_t* src = pool + token_base(ly, layer, page, p & ly.pmask) + kvcol;
+        if constexpr (VROWS) {  // K in operand layout, V as row loads
+            const uint32_t cend = chunk_end(c);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            T.k[m] = ld16(src + 32u * m);
-            T.v[m] = ld16(src + 256u + 32u * m);
+            for (int m = 0; m < 4; ++m) T.k[m] = ld16(src + 32u * m);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t pr = min(t0 + grp + 4u * r, cend);
+                const uint32_t pg = PAGE16 ? page : pt[pr >> ly.log2p];
+                T.v[r] = ld16(pool + token_base(ly, layer, pg, pr & ly.pmask) + 256u +
+                              kvh * kD + 8u * tok);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                T.k[m] = ld16(src + 32u * m);
+                T.v[m] = ld16(src + 256u + 32u * m);
+            }
         }
     };
     // Row-loaded tile -> operand layout (lane (row, group) holds dims
@@ -238,12 +255,12 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // of 16 rows per lane group) spread over all LDS banks. A wave reads only
     // what it wrote, in order: no barrier is needed.
     auto xpose = [&](const Tile& T) -> Tile {
-        if constexpr (!ROWS) return T;
+        if constexpr (!VROWS) return T;
         uint4* xs = s_x[wave];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t t = grp + 4u * r;
-            xs[t * 16u + (tok ^ t)] = T.k[r];
+            if constexpr (ROWS) xs[t * 16u + (tok ^ t)] = T.k[r];
             xs[256u + t * 16u + (tok ^ t)] = T.v[r];
         }
         __builtin_amdgcn_wave_barrier();
@@ -259,7 +276,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const uint32_t x = (4u * m + grp) ^ tok;
-            O.k[m] = xs[tok * 16u + x];
+            O.k[m] = ROWS ? xs[tok * 16u + x] : T.k[m];
             const uint16_t* vr = vs + (((4u * m + (tok & 3u)) ^ vt_tok) * 8u);
             const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) s16x4*)(vr));
@@ -469,7 +486,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 s16x4 vop;
-                if constexpr (ROWS) {  // T.v already holds the V^T operands
+                if constexpr (VROWS) {  // T.v already holds the V^T operands
                     vop = half_s16x4(T.v[m], h);
                 } else {
                     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -534,7 +551,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 F.k[m] = *reinterpret_cast<const uint4*>(&s_fresh[32u * m + 8u * grp]);
-                if constexpr (ROWS) {  // V^T operand: dim d of the token in every k slot
+                if constexpr (VROWS) {  // V^T operand: dim d of the token in every k slot
                     uint32_t w[2];
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
