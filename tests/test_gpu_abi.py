@@ -336,3 +336,48 @@ def test_long_prefill_multichunk(rt, tmp_path, orc):
     assert s.info()["seq_len"] == 20003
     s.close()
     m.close()
+
+
+def test_many_resets_and_two_threads(rt, tmp_path):
+    """Soak-style checks after soak_test.cpp T4 (200 resets) and T2b (two
+    sessions driven from two host threads at once): pages return to zero on
+    every reset, and concurrent sessions produce exactly the tokens they
+    produce when run one after the other."""
+    import threading
+    m = rt.Model(str(tmp_path), rt.model_options(max_context_tokens=1024, max_sessions=4))
+    s = rt.Session(m)
+    cfg = rt.gen_config(max_new_tokens=4, seed=3)
+    for i in range(200):
+        s.prefill([7 + (i % 50)] * (1 + i % 97))
+        s.decode_one(cfg)
+        s.reset()
+        info = s.info()
+        assert info["seq_len"] == 0 and info["pages_owned"] == 0
+    s.close()
+
+    def run(sess, prompt, seed, out):
+        sess.prefill(prompt)
+        c = rt.gen_config(max_new_tokens=40, seed=seed)
+        out.extend(sess.decode_one(c) for _ in range(40))
+
+    prompts = [[11] * 300, [int(x) for x in range(1000, 1200)]]
+    solo = []
+    for i, p in enumerate(prompts):
+        x = rt.Session(m)
+        r = []
+        run(x, p, 100 + i, r)
+        solo.append((r, x.seq(len(p) + 40)))
+        x.close()
+    ss = [rt.Session(m) for _ in prompts]
+    outs = [[], []]
+    th = [threading.Thread(target=run, args=(ss[i], prompts[i], 100 + i, outs[i]))
+          for i in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    for i in range(2):
+        assert outs[i] == solo[i][0]
+        assert ss[i].seq(len(prompts[i]) + 40) == solo[i][1]
+        ss[i].close()
+    m.close()

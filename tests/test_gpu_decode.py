@@ -301,15 +301,20 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed):
     # single-session runs on a second copy of the pool
     d_pool1 = to_dev(pool, dev)
     singles = []
+    parts_b = from_dev(parts, np.float32).reshape(B, 16 * NC * 130)
+    parts2_b = from_dev(parts2, np.float32).reshape(B, 16 * 32 * 130)
     for s in range(B):
         p1 = torch.zeros(16 * NC * 130, dtype=torch.float32, device=dev)
+        p2 = torch.zeros(16 * 32 * 130, dtype=torch.float32, device=dev)
         o1 = torch.zeros(2048, dtype=torch.int16, device=dev)
         kvm.launch_attention_decode(to_dev(q[s], dev), d_lims[s], layer, d_pts[s], d_pool1,
                                     lay, p1, NC, o1, d_inv_freq=inv, chunk_pos=C,
-                                    d_partials2=torch.zeros(16 * 32 * 130,
-                                                            dtype=torch.float32, device=dev))
+                                    d_partials2=p2)
         torch.cuda.synchronize()
         singles.append(from_dev(o1))
+        # partials and level-2 partials too (bytes, so NaN payloads compare)
+        assert np.array_equal(from_dev(p1, np.uint32), parts_b[s].view(np.uint32)), s
+        assert np.array_equal(from_dev(p2, np.uint32), parts2_b[s].view(np.uint32)), s
     assert np.array_equal(got, np.stack(singles)), "batched != single (bitwise)"
     assert np.array_equal(pool_b, from_dev(d_pool1))
     # vs oracle
@@ -333,6 +338,13 @@ def test_batch_vs_single_ctx600(kvm, orc, dev, B, C, ph0):
 
 def test_batch_vs_single_8x2048(kvm, orc, dev):
     _batch_case(kvm, orc, dev, 8, 64, 2047, True, seed=8)
+
+
+@pytest.mark.parametrize("C,ph0", [(64, True), (256, False)])
+def test_batch_vs_single_two_level(kvm, orc, dev, C, ph0):
+    """More than 32 chunks: batched level-1 and level-2 partials and outputs
+    bit-identical to single-session runs."""
+    _batch_case(kvm, orc, dev, 4, C, 9000, ph0, seed=C + 1)
 
 
 @pytest.mark.parametrize("ctx,C,ph0", [(40000, 64, True), (131072, 256, True),
