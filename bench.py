@@ -101,6 +101,20 @@ class Timer:
         t.cuda.synchronize()
         return a.elapsed_time(b) / reps  # ms
 
+    def median(self, fn, reps=30):
+        """Median of `reps` individually timed calls (ms)."""
+        t = self.torch
+        ev = [(t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        t.cuda.synchronize()
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        t.cuda.synchronize()
+        xs = sorted(a.elapsed_time(b) for a, b in ev)
+        return xs[reps // 2]
+
 
 def make_session_pool(torch, dev, n_pages_total, layers):
     """bf16 pool of `layers` layers, values ~N(0,1)/sqrt(128) (bf16 bits as int16)."""
@@ -154,6 +168,7 @@ def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
     chunks_only = timer.capture([chunks_on(p) for p in pools])
     timer.run(step, warmup)
     ms = timer.run(step, steps)
+    ms_med = timer.median(step)
     timer.run(chunks_only, max(1, warmup))
     ms_chunk = timer.run(chunks_only, steps)
     bytes_layer = ctx * KV_BYTES_PER_TOKEN + QO_BYTES
@@ -161,6 +176,7 @@ def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
     return {
         "ctx": ctx, "sessions": 1, "chunk_pos": C, "pages_per_layer": npages,
         "ms_per_step": ms, "us_per_layer": ms * 1e3 / LAYERS,
+        "us_per_layer_median30": ms_med * 1e3 / LAYERS,
         "kv_gbs": bytes_layer * LAYERS / (ms * 1e-3) / 1e9,
         "pct_hbm_peak": 100.0 * bytes_layer * LAYERS / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "tokens_per_s": 1e3 / ms,
@@ -202,10 +218,12 @@ def bench_decode_batch(kvm, torch, dev, timer, B, ctx, steps, warmup):
     step = timer.capture([step_f])
     timer.run(step, warmup)
     ms = timer.run(step, steps)
+    ms_med = timer.median(step)
     bytes_layer = B * (ctx * KV_BYTES_PER_TOKEN + QO_BYTES)
     return {
         "ctx": ctx, "sessions": B, "chunk_pos": C, "ms_per_step": ms,
         "us_per_layer": ms * 1e3 / LAYERS,
+        "us_per_layer_median30": ms_med * 1e3 / LAYERS,
         "kv_gbs": bytes_layer * LAYERS / (ms * 1e-3) / 1e9,
         "pct_hbm_peak": 100.0 * bytes_layer * LAYERS / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "tokens_per_s": B * 1e3 / ms,
