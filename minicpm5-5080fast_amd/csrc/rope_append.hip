@@ -7,12 +7,11 @@
 // p = d mod 64, angle = (float)pos * inv_freq[p].
 //
 // MI355X mapping: one wave64 per token. The 64 lanes first evaluate the 64
-// (cos, sin) pairs of the token once (lane = pair) into LDS. Then lane
-// (g = lane/8, j = lane%8) owns dims [8j, 8j+8) and their rotate partners
-// [64+8j, 64+8j+8) of "head" g, g+8, g+16 (20 heads = 16 q + 2 k + 2 v), so
-// every global access is a 16-byte load/store and 8 lanes cover one 128-byte
-// half-head: fully coalesced. A lane reads both halves before writing either,
-// so the in-place q update has no cross-lane hazard.
+// (cos, sin) pairs of the token once (lane = pair) into LDS. The token row
+// (20 heads of 128 dims: 16 q, 2 k, 2 v) is moved as five 1 KB blocks, lane l
+// holding 16 bytes of each; the rotate partner (dim d ^ 64) is 8 lanes away
+// and comes through a DPP row rotate. All loads precede all stores, so the
+// in-place q update has no cross-lane hazard.
 #include <hip/hip_runtime.h>
 
 #include "error.h"
@@ -24,20 +23,15 @@ namespace {
 
 constexpr uint32_t kWaves = 4;  // tokens per 256-thread block
 
-__device__ __forceinline__ void rotate8(const uint4& lo, const uint4& hi,
-                                        const float* cs, const float* sn,
-                                        uint4& olo, uint4& ohi) {
-    const uint16_t* a = reinterpret_cast<const uint16_t*>(&lo);
-    const uint16_t* b = reinterpret_cast<const uint16_t*>(&hi);
-    uint16_t* oa = reinterpret_cast<uint16_t*>(&olo);
-    uint16_t* ob = reinterpret_cast<uint16_t*>(&ohi);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float x = bf16_to_f32(a[i]);
-        const float x2 = bf16_to_f32(b[i]);
-        oa[i] = f32_to_bf16(rope_rotate(x, x2, cs[i], sn[i], true));
-        ob[i] = f32_to_bf16(rope_rotate(x2, x, cs[i], sn[i], false));
-    }
+// Partner lane of a rotate pair: dims d and d ^ 64 of a head sit 8 lanes
+// apart within a 16-lane DPP row (row_ror:8 swaps lane i and i + 8).
+__device__ __forceinline__ uint4 partner8(const uint4& v) {
+    uint4 r;
+    r.x = (uint32_t)__builtin_amdgcn_mov_dpp((int)v.x, 0x128, 0xF, 0xF, false);
+    r.y = (uint32_t)__builtin_amdgcn_mov_dpp((int)v.y, 0x128, 0xF, 0xF, false);
+    r.z = (uint32_t)__builtin_amdgcn_mov_dpp((int)v.z, 0x128, 0xF, 0xF, false);
+    r.w = (uint32_t)__builtin_amdgcn_mov_dpp((int)v.w, 0x128, 0xF, 0xF, false);
+    return r;
 }
 
 __global__ void __launch_bounds__(256) rope_append_kernel(
@@ -51,25 +45,20 @@ __global__ void __launch_bounds__(256) rope_append_kernel(
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t t = blockIdx.x * kWaves + wave;
     const bool active = t < tokens;
-    const uint32_t g = lane >> 3;  // head group 0..7
-    const uint32_t j = lane & 7u;  // 8-dim block within the half head
-    // Loads are issued in the order their results are needed and none waits
-    // for another: inv_freq (vector), then the row (6 x 16 bytes per lane;
-    // an inactive wave reads token 0's row, lanes past head 19 re-read head
-    // 19), while the base position and the page id come through the scalar
-    // path. The cos/sin evaluation then overlaps the row loads.
+    // Lane l covers bytes [16l, 16l + 16) of each 1 KB block b of the token
+    // row: head 4b + l/16, dims 8*(l%16) .. +7. Every load and store
+    // instruction moves 1 KB contiguous (the K/V block b = 4 is the pool's
+    // 1 KB token row [K h0 | K h1 | V h0 | V h1]).
+    const uint32_t x = lane & 15u;         // 8-dim block within the head
+    const uint32_t pb = 8u * (x & 7u);     // first rotate pair of the lane
+    const bool lo_half = x < 8u;           // dims < 64 of the head
     typedef const __attribute__((address_space(4))) uint32_t* scalar_u32p;
     const float f = inv_freq != nullptr ? inv_freq[lane]
                                         : (float)pow((double)theta, -(double)lane / 64.0);
     uint16_t* row = qkv + (size_t)(active ? t : 0u) * kRow;
-    uint4 lo[3], hi[3];
+    uint4 v[5];
 #pragma unroll
-    for (uint32_t it = 0; it < 3; ++it) {
-        const uint32_t h = min(g + 8u * it, 19u);  // 0..15 q, 16..17 k, 18..19 v
-        const uint16_t* src = row + h * 128u;  // q, k and v heads are contiguous
-        lo[it] = *reinterpret_cast<const uint4*>(src + 8u * j);
-        hi[it] = *reinterpret_cast<const uint4*>(src + 64u + 8u * j);
-    }
+    for (int b = 0; b < 5; ++b) v[b] = *reinterpret_cast<const uint4*>(row + 512u * b + 8u * lane);
     const uint32_t base = *(scalar_u32p)d_base_pos;
     const uint32_t pos = base + t;
     const uint32_t tok_pos = __builtin_amdgcn_readfirstlane(active ? pos : base);
@@ -86,27 +75,25 @@ __global__ void __launch_bounds__(256) rope_append_kernel(
     float cs[8], sn[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        cs[i] = s_cs[wave][8u * j + i];
-        sn[i] = s_sn[wave][8u * j + i];
+        cs[i] = s_cs[wave][pb + i];
+        sn[i] = s_sn[wave][pb + i];
     }
     uint16_t* dst = pool + token_base(ly, layer, page, pos & ly.pmask);
-
 #pragma unroll
-    for (uint32_t it = 0; it < 3; ++it) {
-        const uint32_t h = g + 8u * it;
-        if (h >= 20u) break;
-        uint16_t* src = row + h * 128u;
-        if (h < 18u) {
-            uint4 olo, ohi;
-            rotate8(lo[it], hi[it], cs, sn, olo, ohi);
-            uint16_t* o = (h < 16u) ? src : dst + (h - 16u) * 128u;
-            *reinterpret_cast<uint4*>(o + 8u * j) = olo;
-            *reinterpret_cast<uint4*>(o + 64u + 8u * j) = ohi;
-        } else {
-            uint16_t* o = dst + 256u + (h - 18u) * 128u;
-            *reinterpret_cast<uint4*>(o + 8u * j) = lo[it];
-            *reinterpret_cast<uint4*>(o + 64u + 8u * j) = hi[it];
+    for (int b = 0; b < 5; ++b) {
+        const uint4 p2 = partner8(v[b]);
+        uint4 o = v[b];
+        if (b < 4 || lane < 32u) {  // q heads, k heads: rotate; v heads: copy
+            const uint16_t* a = reinterpret_cast<const uint16_t*>(&v[b]);
+            const uint16_t* a2 = reinterpret_cast<const uint16_t*>(&p2);
+            uint16_t* oo = reinterpret_cast<uint16_t*>(&o);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                oo[i] = f32_to_bf16(rope_rotate(bf16_to_f32(a[i]), bf16_to_f32(a2[i]), cs[i],
+                                                sn[i], lo_half));
         }
+        uint16_t* out = b < 4 ? row + 512u * b : dst;
+        *reinterpret_cast<uint4*>(out + 8u * lane) = o;
     }
 }
 
