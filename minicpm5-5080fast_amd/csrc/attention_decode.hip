@@ -147,7 +147,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                                                   const float* __restrict__ inv_freq,
                                                   uint32_t C, uint32_t kvh,
                                                   uint32_t c_first, uint32_t cpw) {
-    __shared__ float s_cs[64], s_sn[64];
+    __shared__ __align__(16) uint16_t s_q[PH0 ? kGroup * kD : 1];  // rotated q rows
     __shared__ __align__(16) uint16_t s_fresh[256];  // phase0: K | V of `limit`
     __shared__ uint32_t s_pages[kPageCache];         // page ids of this block's range
     constexpr bool ROWS = MCKV_ROW_LOADS && (TPW == 1u || (MCKV_K_ROW_ALL && TPW > 1u));
@@ -324,11 +324,23 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // All start-up loads are unconditional (addresses clamped) so that no
     // divergent branch makes the compiler wait for them before the first
     // K/V tiles are issued.
+    // q: without phase0 each lane loads its Q^T operand directly; with phase0
+    // thread tid loads dims p and p + 64 (p = tid % 64) of heads 2w, 2w + 1
+    // (w = tid / 64) of this KV head, rotates them with pair p and stages the
+    // rotated rows in LDS (4 rotations per thread instead of 32 per lane).
     uint4 qr[4];
-    {
+    uint16_t qx[2][2];  // phase0: [head 2w + hh][dim p, p + 64]
+    if constexpr (!PH0) {
         const uint16_t* qsrc = q_row + (kvh * kGroup + (real ? tok : 0u)) * kD + 8u * grp;
 #pragma unroll
         for (int m = 0; m < 4; ++m) qr[m] = *reinterpret_cast<const uint4*>(qsrc + 32u * m);
+    } else {
+        const uint16_t* qh0 = q_row + (kvh * kGroup + 2u * wave) * kD + (tid & 63u);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            qx[hh][0] = qh0[hh * kD];
+            qx[hh][1] = qh0[hh * kD + 64u];
+        }
     }
     const uint32_t t64 = tid & 63u;
     float invf = 0.f;
@@ -368,58 +380,52 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     }
 
     if (cached_pages && tid < npages_rng) s_pages[tid] = staged_page;
-    if (tid < 64u) {
-        if (PH0) {
-            float c, sn;
-            rope_sincos((float)limit * invf, &c, &sn);
-            s_cs[tid] = c;
-            s_sn[tid] = sn;
-            if (owner) {  // pair tid rotates dims tid and tid + 64
-                const float x = bf16_to_f32(kx), x2 = bf16_to_f32(kx2);
-                const uint16_t lo = f32_to_bf16(rope_rotate(x, x2, c, sn, true));
-                const uint16_t hi = f32_to_bf16(rope_rotate(x2, x, c, sn, false));
-                s_fresh[tid] = lo;
-                s_fresh[tid + 64u] = hi;
-                *reinterpret_cast<uint32_t*>(&s_fresh[128u + 2u * tid]) = fresh_v;
-                uint16_t* dst =
-                    pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
-                dst[tid] = lo;
-                dst[tid + 64u] = hi;
-                *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = fresh_v;
-            }
-        } else if (owner) {
-            const uint32_t h = tid >> 5, d = (tid & 31u) * 4u;
-            *reinterpret_cast<uint2*>(&s_fresh[128u * h + d]) = fresh_kv;
+    if (PH0) {
+        // cos/sin of pair p = tid % 64 (every wave evaluates the same 64)
+        float c, sn;
+#ifdef MCKV_PROBE_NO_SINCOS
+        c = 1.f + (float)limit * invf * 1e-30f;
+        sn = 0.f;
+#else
+        rope_sincos((float)limit * invf, &c, &sn);
+#endif
+        const uint32_t p = tid & 63u;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const float x = bf16_to_f32(qx[hh][0]), x2 = bf16_to_f32(qx[hh][1]);
+            uint16_t* qd = &s_q[(2u * wave + hh) * kD + p];
+            qd[0] = f32_to_bf16(rope_rotate(x, x2, c, sn, true));
+            qd[64] = f32_to_bf16(rope_rotate(x2, x, c, sn, false));
         }
+        if (owner && tid < 64u) {  // pair tid rotates dims tid and tid + 64 of k
+            const float x = bf16_to_f32(kx), x2 = bf16_to_f32(kx2);
+            const uint16_t lo = f32_to_bf16(rope_rotate(x, x2, c, sn, true));
+            const uint16_t hi = f32_to_bf16(rope_rotate(x2, x, c, sn, false));
+            s_fresh[tid] = lo;
+            s_fresh[tid + 64u] = hi;
+            *reinterpret_cast<uint32_t*>(&s_fresh[128u + 2u * tid]) = fresh_v;
+            uint16_t* dst =
+                pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
+            dst[tid] = lo;
+            dst[tid + 64u] = hi;
+            *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = fresh_v;
+        }
+    } else if (owner && tid < 64u) {
+        const uint32_t h = tid >> 5, d = (tid & 31u) * 4u;
+        *reinterpret_cast<uint2*>(&s_fresh[128u * h + d]) = fresh_kv;
     }
     __syncthreads();
 
     // Q^T B operand: lane holds q[head = tok][32m + 8*grp + i]; heads >= 8 zero.
-    // Phase0 rotates q in registers (partner dim d^64 sits in block m^2).
     bf16x8 qb[4];
-    {
-        if (PH0 && real) {
-            uint4 rq[4];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const uint16_t* x = reinterpret_cast<const uint16_t*>(&qr[m]);
-                const uint16_t* x2 = reinterpret_cast<const uint16_t*>(&qr[m ^ 2]);
-                uint16_t* o = reinterpret_cast<uint16_t*>(&rq[m]);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t pr = 32u * (m & 1) + 8u * grp + i;
-                    o[i] = f32_to_bf16(rope_rotate(bf16_to_f32(x[i]),
-                                                   bf16_to_f32(x2[i]), s_cs[pr],
-                                                   s_sn[pr], m < 2));
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < 4; ++m) qr[m] = rq[m];
-        }
+    if constexpr (PH0) {
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            qb[m] = as_bf16x8(real ? qr[m] : make_uint4(0u, 0u, 0u, 0u));
+            qr[m] = *reinterpret_cast<const uint4*>(
+                &s_q[(real ? tok : 0u) * kD + 32u * m + 8u * grp]);
     }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) qb[m] = as_bf16x8(real ? qr[m] : make_uint4(0u, 0u, 0u, 0u));
 
     // Identity B operand for the transpose: B[k][c] = (k == c), k = 4*grp + i.
     s16x4 ident;
