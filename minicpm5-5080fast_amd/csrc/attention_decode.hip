@@ -893,9 +893,13 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
 #ifndef MCKV_TARGET_BLOCKS
 #define MCKV_TARGET_BLOCKS 512
 #endif
-uint32_t chunks_per_block(uint32_t NC, uint32_t C) {
+#ifndef MCKV_BATCH_TARGET_BLOCKS
+#define MCKV_BATCH_TARGET_BLOCKS MCKV_TARGET_BLOCKS
+#endif
+uint32_t chunks_per_block(uint32_t NC, uint32_t C, bool batched) {
     if (C % 64u != 0u) return 1u;
-    const uint32_t cpw = NC * kHkv / MCKV_TARGET_BLOCKS;
+    const uint32_t cpw =
+        NC * kHkv / (batched ? MCKV_BATCH_TARGET_BLOCKS : MCKV_TARGET_BLOCKS);
     return cpw < 1u ? 1u : cpw;
 }
 
@@ -906,7 +910,7 @@ mc_status_t launch_chunks(const uint16_t* q, const uint32_t* d_pos,
                           uint16_t* pool, uint16_t* const* slot_kv, DevLayout ly,
                           float* partials, uint32_t NC, uint16_t* out,
                           hipStream_t st, const float* inv_freq, uint32_t C) {
-    const uint32_t cpw = chunks_per_block(NC, C);
+    const uint32_t cpw = chunks_per_block(NC, C, BATCH);
     const dim3 grid((NC + cpw - 1u) / cpw, kHkv, B);
 #define MCKV_LAUNCH_CHUNK(PH, PG, TP)                                                      \
     hipLaunchKernelGGL((decode_chunk_kernel<PH, BATCH, PG, TP>), grid, dim3(kThreads), 0, st, \
