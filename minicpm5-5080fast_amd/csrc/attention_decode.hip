@@ -91,6 +91,9 @@ constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 #ifndef MCKV_V_ROW_LOADS
 #define MCKV_V_ROW_LOADS 1  // V row loads (+ transposing LDS reads) also for C > 64
 #endif
+#ifndef MCKV_V_ROW_MIN_TPW
+#define MCKV_V_ROW_MIN_TPW 2u  // smallest tiles-per-wave tier using V row loads
+#endif
 #ifndef MCKV_NT_LOADS
 #define MCKV_NT_LOADS 0
 #endif
@@ -151,7 +154,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     __shared__ __align__(16) uint16_t s_fresh[256];  // phase0: K | V of `limit`
     __shared__ uint32_t s_pages[kPageCache];         // page ids of this block's range
     constexpr bool ROWS = MCKV_ROW_LOADS && (TPW == 1u || (MCKV_K_ROW_ALL && TPW > 1u));
-    constexpr bool VROWS = ROWS || (MCKV_V_ROW_LOADS && TPW > 1u);  // V row loads
+    constexpr bool VROWS = ROWS || (MCKV_V_ROW_LOADS && TPW >= MCKV_V_ROW_MIN_TPW);
     // per wave: K and V tile, 16 x 256 B (row loads only)
     __shared__ uint4 s_x[VROWS ? kWaves : 1u][VROWS ? 2u * 16u * 16u : 1u];
     __shared__ float s_m[kFoldSlots][kWaves][kGroup], s_l[kFoldSlots][kWaves][kGroup];
