@@ -20,28 +20,30 @@
 //     the 32 level-2 partials and writes bf16(A/L).
 //   * Phase0 (inv_freq != NULL): the block owning position `limit` rotates that
 //     token's k from the qkv row, writes K and V of `limit` to the pool and uses
-//     the fresh values; q is rotated in registers and never written back.
+//     the fresh values; q is rotated on the fly (LDS) and never written back.
 //
 // MI355X design (one 256-thread workgroup = 4 wave64 per (slot, kv head,
-// chunk)). Each wave walks 16-position tiles t = wave, wave+4, ... of its chunk
-// and keeps its own online-softmax state for all 8 query heads of the KV head;
-// the 4 wave states are folded through LDS at the end. Per tile a lane
-// (token = lane%16, group = lane/16) issues eight 16-byte global loads: K and V
-// dims [32m + 8*group, +8) for m = 0..3 of its token, i.e. each instruction
-// reads 64 contiguous bytes of 16 rows; the next tile's loads are in flight
-// while the current tile computes.
-//   * QK: S^T[16 pos][16 heads] = K (A operand, exactly the loaded registers)
-//     x Q^T (B operand, preloaded; heads 8..15 are zero padding) with four
-//     v_mfma_f32_16x16x32_bf16.
+// range of chunks)). Each wave walks 16-position tiles t = wave, wave+4, ...
+// of each chunk and keeps its own online-softmax state for all 8 query heads
+// of the KV head; the 4 wave states are folded through LDS per chunk. The next
+// tile's loads are in flight while the current tile computes.
+//   * Loads: K in operand layout - a lane (token = lane%16, group = lane/16)
+//     reads K dims [32m + 8*group, +8), m < 4, i.e. each instruction reads 64
+//     contiguous bytes of 16 rows. V as whole 256-byte head rows (16 lanes per
+//     row) into a wave-private, XOR-swizzled LDS tile. For the 64-position
+//     chunk tier K is row-loaded the same way and read back from LDS in the
+//     operand layout.
+//   * QK: S^T[16 pos][16 heads] = K (A operand) x Q^T (B operand, preloaded;
+//     heads 8..15 are zero padding) with four v_mfma_f32_16x16x32_bf16.
 //   * The D layout gives each lane 4 positions of one head; the batch max/sum
 //     need two cross-lane xor steps (16, 32).
-//   * P.V needs V with positions along the contraction, but the loaded V has
-//     dims along lanes. Multiplying the loaded 16x16 V block by an identity
-//     B operand (v_mfma_f32_16x16x16bf16_1k) transposes it exactly (every D
-//     element is one bf16 value times 1.0); the truncated result is the A
-//     operand of O^T += V^T x P^T, whose B operand (P^T) is the softmax output
-//     already in the right lanes. acc ends up as 32 fp32 per lane: head
-//     lane%16, dims [32m + 8*group, +8) - the dims the lane loaded.
+//   * P.V: O^T += V^T x P^T (v_mfma_f32_16x16x16bf16_1k). The V^T A operand
+//     comes from the LDS tile through the transposing read ds_read_b64_tr_b16;
+//     P^T (B operand) is the softmax output already in the right lanes. (The
+//     generic schedule for chunk sizes that are not a multiple of 64 keeps V in
+//     operand layout and transposes each 16x16 block exactly by an MFMA with an
+//     identity B operand.) acc ends up as 32 fp32 per lane: head lane%16, dims
+//     [32m + 8*group, +8).
 // Arithmetic intensity is ~8 flop/byte, so the kernel is HBM-bound; MFMA keeps
 // the VALU free for addressing and softmax.
 #include <hip/hip_runtime.h>
