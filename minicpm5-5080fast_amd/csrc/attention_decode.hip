@@ -56,6 +56,17 @@
 
 namespace mckv {
 namespace {
+// Timing probe (off by default): -DMCKV_PROBE_TIMES records, per workgroup of
+// the chunk kernel, the 100 MHz real-time clock at entry (row 0), after the
+// start-up barrier (1), at the first chunk fold (2) and at exit (3), plus the
+// HW_ID (4) and XCC_ID (5) registers, read back with mckv_probe_read().
+#ifdef MCKV_PROBE_TIMES
+__device__ unsigned long long g_probe_t[6][8192];
+#define PROBE_T(i) do { if (threadIdx.x == 0u) { __builtin_amdgcn_s_waitcnt(0); \
+    g_probe_t[i][blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_memrealtime(); } } while (0)
+#else
+#define PROBE_T(i) do {} while (0)
+#endif
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -77,6 +88,9 @@ constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 #endif
 #ifndef MCKV_WAVES_PER_EU
 #define MCKV_WAVES_PER_EU 2
+#endif
+#ifndef MCKV_KV2_MIN_BLOCKS
+#define MCKV_KV2_MIN_BLOCKS 256u
 #endif
 #ifndef MCKV_RING
 #define MCKV_RING 2
@@ -139,34 +153,46 @@ struct DecodeArgs {
     uint16_t* out;    // this slot: [2048]
 };
 
-// One workgroup processes chunks [c_first, c_first + cpw) of one (slot, kv
-// head). Waves take tiles j = wave, wave+4, ... of each chunk; the next tile's
-// loads are issued before the current tile computes, also across a chunk
-// boundary, so the memory pipeline never drains between chunks. At the end of
-// every chunk the 4 wave states are folded through LDS (double-buffered by
-// chunk parity, one barrier per chunk) and the partial (or, for a single-chunk
-// context, the output) is written. cpw > 1 requires C % 64 == 0.
-template <bool PH0, bool PAGE16, uint32_t TPW>
+// 256 threads process chunks [c_first, c_first + cpw) of one (slot, kv head);
+// with KV2 the workgroup has 512 threads and threads 256-511 run the same
+// body for the second KV head over the same chunks (separate LDS). Waves take
+// tiles j = wave, wave+4, ... of each chunk; the next tile's loads are issued
+// before the current tile computes, also across a chunk boundary, so the
+// memory pipeline never drains between chunks. Each wave stashes its state
+// of a finished chunk in LDS; every kFoldSlots chunks (and at the end) the 4
+// wave states are folded in fixed wave order and the partials (or, for a
+// single-chunk context, the output) are written. cpw > 1 requires
+// C % 64 == 0.
+template <bool PH0, bool PAGE16, uint32_t TPW, bool KV2>
 __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t layer,
                                                   DevLayout ly, uint32_t NC,
                                                   const float* __restrict__ inv_freq,
                                                   uint32_t C, uint32_t kvh,
                                                   uint32_t c_first, uint32_t cpw) {
-    __shared__ __align__(16) uint16_t s_q[PH0 ? kGroup * kD : 1];  // rotated q rows
-    __shared__ __align__(16) uint16_t s_fresh[256];  // phase0: K | V of `limit`
-    __shared__ uint32_t s_pages[kPageCache];         // page ids of this block's range
+    constexpr uint32_t NH = KV2 ? 2u : 1u;  // kv heads per workgroup
+    const uint32_t half = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : 0u;
     constexpr bool ROWS = MCKV_ROW_LOADS && (TPW == 1u || (MCKV_K_ROW_ALL && TPW > 1u));
     constexpr bool VROWS = ROWS || (MCKV_V_ROW_LOADS && TPW >= MCKV_V_ROW_MIN_TPW);
+    __shared__ __align__(16) uint16_t s_q_[NH][PH0 ? kGroup * kD : 1];  // rotated q rows
+    __shared__ __align__(16) uint16_t s_fresh_[NH][256];  // phase0: K | V of `limit`
+    __shared__ uint32_t s_pages_[NH][kPageCache];         // page ids of this block's range
     // per wave: K and V tile, 16 x 256 B (row loads only)
-    __shared__ uint4 s_x[VROWS ? kWaves : 1u][VROWS ? 2u * 16u * 16u : 1u];
-    __shared__ float s_m[kFoldSlots][kWaves][kGroup], s_l[kFoldSlots][kWaves][kGroup];
-    __shared__ __align__(16) float s_acc[kFoldSlots][kWaves][kGroup][kD];
+    __shared__ uint4 s_x_[NH][VROWS ? kWaves : 1u][VROWS ? 2u * 16u * 16u : 1u];
+    __shared__ float s_m_[NH][kFoldSlots][kWaves][kGroup], s_l_[NH][kFoldSlots][kWaves][kGroup];
+    __shared__ __align__(16) float s_acc_[NH][kFoldSlots][kWaves][kGroup][kD];
+    auto& s_q = s_q_[half];
+    auto& s_fresh = s_fresh_[half];
+    auto& s_pages = s_pages_[half];
+    auto& s_x = s_x_[half];
+    auto& s_m = s_m_[half];
+    auto& s_l = s_l_[half];
+    auto& s_acc = s_acc_[half];
 
     const uint32_t limit = a.limit;
     const uint32_t nvalid = min(limit / C + 1u, NC);
     if (c_first >= nvalid) return;  // uniform over the block
     const uint32_t c_end = min(c_first + cpw, nvalid);
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = threadIdx.x & 255u;
     // Wave index made provably wave-uniform so every tile / chunk decision
     // below compiles to scalar branches.
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -420,6 +446,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         *reinterpret_cast<uint2*>(&s_fresh[128u * h + d]) = fresh_kv;
     }
     __syncthreads();
+    PROBE_T(1);
 
     // Q^T B operand: lane holds q[head = tok][32m + 8*grp + i]; heads >= 8 zero.
     bf16x8 qb[4];
@@ -559,7 +586,13 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         nstash = 0;
         if (cc < c_end) __syncthreads();  // slots are reused by later chunks
     };
+#ifdef MCKV_PROBE_TIMES
+    bool probe_first = true;
+#endif
     auto fold = [&]() {
+#ifdef MCKV_PROBE_TIMES
+        if (probe_first) { PROBE_T(2); probe_first = false; }
+#endif
         if (owner && wave == 0u && cc == limit / C) {
             Tile F;
 #pragma unroll
@@ -660,17 +693,24 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #else
 #define MCKV_CHUNK_ATTR
 #endif
-// grid = (ceil(NC / cpw), 2 kv heads, B slots). Single-session launches pass
+// grid = (ceil(NC / cpw), 2 kv heads (1 with KV2), B slots). Single-session launches pass
 // B = 1 and the direct pointers; batched launches resolve per-slot pointers
 // from device tables.
-template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW>
-__global__ void __launch_bounds__(kThreads) MCKV_CHUNK_ATTR decode_chunk_kernel(
+template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2>
+__global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR decode_chunk_kernel(
     const uint16_t* __restrict__ q_rows, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t layer,
     const uint32_t* pt, const uint32_t* const* __restrict__ slot_pt,
     uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
     float* __restrict__ partials, uint32_t NC, uint16_t* __restrict__ out,
     const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw) {
+    PROBE_T(0);
+#ifdef MCKV_PROBE_TIMES
+    if (threadIdx.x == 0u) {
+        g_probe_t[4][blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_getreg(63492);
+        g_probe_t[5][blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_getreg(6164);
+    }
+#endif
     const uint32_t slot = blockIdx.z;
     DecodeArgs a;
     a.q_row = q_rows + (size_t)slot * kRow;
@@ -679,8 +719,13 @@ __global__ void __launch_bounds__(kThreads) MCKV_CHUNK_ATTR decode_chunk_kernel(
     a.pool = BATCH ? slot_kv[slot] : pool;
     a.partials = partials + (size_t)slot * kHq * NC * kPartial;
     a.out = out + (size_t)slot * kHq * kD;
-    decode_range_body<PH0, PAGE16, TPW>(a, layer, ly, NC, inv_freq, C, blockIdx.y,
+    const uint32_t kvh = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : blockIdx.y;
+    decode_range_body<PH0, PAGE16, TPW, KV2>(a, layer, ly, NC, inv_freq, C, kvh,
                                    blockIdx.x * cpw, cpw);
+#ifdef MCKV_PROBE_TIMES
+    __syncthreads();
+    PROBE_T(3);
+#endif
 }
 
 __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
@@ -916,17 +961,33 @@ mc_status_t launch_chunks(const uint16_t* q, const uint32_t* d_pos,
                           float* partials, uint32_t NC, uint16_t* out,
                           hipStream_t st, const float* inv_freq, uint32_t C) {
     const uint32_t cpw = chunks_per_block(NC, C, BATCH);
-    const dim3 grid((NC + cpw - 1u) / cpw, kHkv, B);
-#define MCKV_LAUNCH_CHUNK(PH, PG, TP)                                                      \
-    hipLaunchKernelGGL((decode_chunk_kernel<PH, BATCH, PG, TP>), grid, dim3(kThreads), 0, st, \
+    const uint32_t nx = (NC + cpw - 1u) / cpw;
+    // Both KV heads in one 512-thread workgroup when that still gives every
+    // CU a workgroup: the 8 waves of a CU then stream the same token rows at
+    // the same pace (two independent workgroups per CU finish several us
+    // apart, and the later one runs alone at half the loads in flight).
+    // Batched launches keep one head per workgroup: their ragged slots leave
+    // many workgroups short, and finer ones balance better (measured).
+    const bool kv2 = !BATCH && (C == 256u || C == 512u) && nx >= MCKV_KV2_MIN_BLOCKS;
+    const dim3 grid(nx, kv2 ? 1u : kHkv, B);
+    const dim3 block(kv2 ? kHkv * kThreads : kThreads);
+#define MCKV_LAUNCH_CHUNK_KV(PH, PG, TP, KV)                                                 \
+    hipLaunchKernelGGL((decode_chunk_kernel<PH, BATCH, PG, TP, KV>), grid, block, 0, st,     \
                        q, d_pos, slot_pos, layer, pt, slot_pt, pool, slot_kv, ly, partials,  \
                        NC, out, inv_freq, C, cpw)
+#define MCKV_LAUNCH_CHUNK(PH, PG, TP) MCKV_LAUNCH_CHUNK_KV(PH, PG, TP, false)
 #define MCKV_LAUNCH_TPW(PH, PG)                          \
     switch (C) {                                         \
         case 64: MCKV_LAUNCH_CHUNK(PH, PG, 1u); break;   \
         case 128: MCKV_LAUNCH_CHUNK(PH, PG, 2u); break;  \
-        case 256: MCKV_LAUNCH_CHUNK(PH, PG, 4u); break;  \
-        case 512: MCKV_LAUNCH_CHUNK(PH, PG, 8u); break;  \
+        case 256:                                        \
+            if (kv2) MCKV_LAUNCH_CHUNK_KV(PH, PG, 4u, true); \
+            else MCKV_LAUNCH_CHUNK(PH, PG, 4u);          \
+            break;                                       \
+        case 512:                                        \
+            if (kv2) MCKV_LAUNCH_CHUNK_KV(PH, PG, 8u, true); \
+            else MCKV_LAUNCH_CHUNK(PH, PG, 8u);          \
+            break;                                       \
         default: MCKV_LAUNCH_CHUNK(PH, PG, 0u); break;   \
     }
     const bool page16 = ly.log2p >= 4u;
@@ -939,6 +1000,7 @@ mc_status_t launch_chunks(const uint16_t* q, const uint32_t* d_pos,
     }
 #undef MCKV_LAUNCH_TPW
 #undef MCKV_LAUNCH_CHUNK
+#undef MCKV_LAUNCH_CHUNK_KV
     return check_launch("decode attention chunk launch failed");
 }
 
@@ -977,6 +1039,11 @@ bool chunk_args_ok(uint32_t max_chunks, uint32_t chunk_pos) {
 
 }  // namespace
 }  // namespace mckv
+#ifdef MCKV_PROBE_TIMES
+extern "C" __attribute__((visibility("default"))) int mckv_probe_read(void* host) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(mckv::g_probe_t), sizeof(mckv::g_probe_t));
+}
+#endif
 
 using namespace mckv;
 

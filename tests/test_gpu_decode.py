@@ -347,6 +347,13 @@ def test_batch_vs_single_two_level(kvm, orc, dev, C, ph0):
     _batch_case(kvm, orc, dev, 4, C, 9000, ph0, seed=C + 1)
 
 
+def test_batch_vs_single_both_heads_per_workgroup(kvm, orc, dev):
+    """128K tier (C = 256, 512 chunks): single-session launches put both KV
+    heads in one 512-thread workgroup, batched launches one head per
+    workgroup; partials, level-2 partials and outputs stay bit-identical."""
+    _batch_case(kvm, orc, dev, 2, 256, 131000, True, seed=0x2C4)
+
+
 @pytest.mark.parametrize("ctx,C,ph0", [(40000, 64, True), (131072, 256, True),
                                        (70001, 256, False)])
 def test_decode_long_multichunk_blocks(kvm, orc, dev, ctx, C, ph0):
