@@ -63,7 +63,8 @@ namespace {
 #ifdef MCKV_PROBE_TIMES
 __device__ unsigned long long g_probe_t[6][8192];
 #define PROBE_T(i) do { if (threadIdx.x == 0u) { __builtin_amdgcn_s_waitcnt(0); \
-    g_probe_t[i][blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_memrealtime(); } } while (0)
+    g_probe_t[i][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = \
+    __builtin_amdgcn_s_memrealtime(); } } while (0)
 #else
 #define PROBE_T(i) do {} while (0)
 #endif
@@ -640,10 +641,12 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         // Straight-line schedule (C == 64 * TPW): wave w owns tiles
         // j = w + 4i, i < TPW, of every chunk. Chunks are walked in pairs with
         // the tile loop fully unrolled, so the ring slot of every tile is a
-        // compile-time constant and the load of the next tile is always
-        // issued (clamped to an already-fetched tile past the range end)
+        // compile-time constant and the load of the next tile is issued
         // before the current one computes; the wait before each compute then
-        // covers only the older load group.
+        // covers only the older load group. Loads for chunks past the range
+        // are skipped (scalar branch; the compiler's wait counts stay
+        // conservative across it), tiles past a chunk's end within the range
+        // are clamped to an already-fetched tile and never accumulated.
         // Ring of MCKV_RING register tiles, MCKV_RING - 1 loads ahead; U
         // chunks are unrolled per loop trip so that U * TPW is a multiple of
         // the ring size and every slot index is a compile-time constant.
@@ -657,7 +660,8 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                 for (uint32_t i = 0; i < TPW; ++i) {
                     const uint32_t g = h * TPW + i;
                     const uint32_t ga = g + RING - 1u;  // tile to prefetch
-                    clamp_load(R[ga % RING], c + ga / TPW, ga % TPW, false);
+                    if (c + ga / TPW < c_end)
+                        clamp_load(R[ga % RING], c + ga / TPW, ga % TPW, false);
                     const uint32_t j = wave + 4u * i;
                     if (cc2 < c_end && j < chunk_tiles(cc2)) {
                         while (cc < cc2) fold();
@@ -707,8 +711,8 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR
     PROBE_T(0);
 #ifdef MCKV_PROBE_TIMES
     if (threadIdx.x == 0u) {
-        g_probe_t[4][blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_getreg(63492);
-        g_probe_t[5][blockIdx.x + gridDim.x * blockIdx.y] = __builtin_amdgcn_s_getreg(6164);
+        g_probe_t[4][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = __builtin_amdgcn_s_getreg(63492);
+        g_probe_t[5][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = __builtin_amdgcn_s_getreg(6164);
     }
 #endif
     const uint32_t slot = blockIdx.z;
