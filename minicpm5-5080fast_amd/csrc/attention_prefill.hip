@@ -53,6 +53,18 @@ constexpr uint32_t kThreads = 512;
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) {
     return __builtin_bit_cast(bf16x8, u);
 }
+// Max over the 4 lanes l, l^16, l^32, l^48 with gfx950's row-swap permutes
+// (VALU, no LDS round trip): permlane16_swap(x, x) yields rows (0,0,2,2) and
+// (1,1,3,3) of x, permlane32_swap(y, y) the halves (lo,lo) and (hi,hi).
+__device__ __forceinline__ float max_across_groups(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y),
+                                                    false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 constexpr uint32_t kQRows = 32;  // q rows per workgroup
 #ifndef PF_STEP
 #define PF_STEP 64
@@ -275,8 +287,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
             for (int kb = 0; kb < kNKB; ++kb)
                 tm = fmaxf(tm, fmaxf(fmaxf(sacc[kb][g][0], sacc[kb][g][1]),
                                      fmaxf(sacc[kb][g][2], sacc[kb][g][3])));
-            tm = fmaxf(tm, __shfl_xor(tm, 16));
-            tm = fmaxf(tm, __shfl_xor(tm, 32));
+            tm = max_across_groups(tm);
             const float mn = fmaxf(m_run[g], tm);
             // Lazy reference point: m_run moves only when the new max exceeds
             // it by more than 8 in log2 units (p <= 2^8 otherwise) or when it
