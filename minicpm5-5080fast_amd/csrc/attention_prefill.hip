@@ -122,11 +122,16 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         }
     }
 
-    float m_run[G], l_run[G], ren[G];
+    // Per column: running reference max m_run (raw score units), the score
+    // above which it moves (thr = m_run + 8 / kC) and nmc = -m_run * kC
+    // (0 while m_run is -inf), all updated only when the reference moves.
+    float m_run[G], l_run[G], ren[G], thr[G], nmc[G];
     f32x4 acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m_run[g] = -INFINITY;
+        thr[g] = -INFINITY;
+        nmc[g] = 0.f;
         l_run[g] = 0.f;
 #pragma unroll
         for (int db = 0; db < 8; ++db) acc[g][db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -157,6 +162,27 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         }
     };
     auto gather = [&](uint32_t js, const uint32_t (&pg)[2 * kNH]) {
+        if constexpr (PAGE_STEP) {
+            // The step lies in one page: scalar page base, 32-bit lane offsets,
+            // and no per-lane range test unless the step passes key_end.
+            const uint16_t* pbase = pool + token_base(ly, layer, pg[0], 0u);
+            const uint32_t step0 = js * kStep;
+            const bool full = step0 + kStep - 1u <= key_end;  // wave-uniform
+#pragma unroll
+            for (int r = 0; r < 2 * kNH; ++r) {
+                const uint32_t key = 32u * (r % kNH) + kkey;
+                const uint32_t off = ((step0 + key) & ly.pmask) * kSlotElems +
+                                     (r >= kNH ? 256u : 0u) + kvh * kD + kdb * 8u;
+                if (full) {
+                    stage[r] = *reinterpret_cast<const uint4*>(pbase + off);
+                } else {
+                    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                    if (step0 + key <= key_end) v = *reinterpret_cast<const uint4*>(pbase + off);
+                    stage[r] = v;
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < 2 * kNH; ++r) {
             const bool isv = r >= kNH;
@@ -190,6 +216,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     // raw scores (c > 0). l is kept per lane (its own 8 keys per step) and
     // summed across the 4 lane groups at the end.
     constexpr float kC = kScoreScale * 1.4426950408889634f;
+    constexpr float kMoveSlack = 8.f / kC;  // 8 in log2 units, in raw score units
     uint32_t pgn[2 * kNH] = {};
     if (js0 <= js1) {
         page_ids(js0, pgn);
@@ -288,30 +315,31 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
                 tm = fmaxf(tm, fmaxf(fmaxf(sacc[kb][g][0], sacc[kb][g][1]),
                                      fmaxf(sacc[kb][g][2], sacc[kb][g][3])));
             tm = max_across_groups(tm);
-            const float mn = fmaxf(m_run[g], tm);
             // Lazy reference point: m_run moves only when the new max exceeds
             // it by more than 8 in log2 units (p <= 2^8 otherwise) or when it
-            // is still -inf; softmax is invariant to the reference point, so
-            // this changes rounding only and leaves most steps without the
-            // acc rescale. Column-uniform (mn, m_run agree across lane groups).
-            const bool move = (m_run[g] == -INFINITY) ? (mn != -INFINITY)
-                                                     : ((mn - m_run[g]) * kC > 8.f);
+            // is still -inf (thr = -inf: any finite max moves it); softmax is
+            // invariant to the reference point, so this changes rounding only
+            // and leaves most steps without the acc rescale. Column-uniform
+            // (tm, m_run agree across lane groups). A moving max exceeds
+            // m_run, so the new reference is tm itself; from m_run = -inf the
+            // factor exp2(-inf) is 0.
             ren[g] = 1.f;
-            if (move) {
-                const float renew =
-                    (m_run[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run[g] - mn) * kC);
+            if (tm > thr[g]) {
+                const float renew = __builtin_amdgcn_exp2f((m_run[g] - tm) * kC);
                 l_run[g] *= renew;
-                m_run[g] = mn;
+                m_run[g] = tm;
+                thr[g] = tm + kMoveSlack;
+                nmc[g] = -tm * kC;
                 ren[g] = renew;
             }
-            // fully masked so far (m_run = -inf): p = 0 and the state is kept
-            const float nmc = (m_run[g] == -INFINITY) ? 0.f : -m_run[g] * kC;
+            // fully masked so far (m_run = -inf, nmc = 0): every score is -inf,
+            // p = 0 and the state is kept
             float ls = 0.f;
 #pragma unroll
             for (int kb = 0; kb < kNKB; ++kb)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][g][j], kC, nmc));
+                    const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][g][j], kC, nmc[g]));
                     ls += p;
                     pb[g][kb >> 1][4 * (kb & 1) + j] = (__bf16)p;
                 }
