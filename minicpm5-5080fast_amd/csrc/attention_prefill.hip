@@ -229,7 +229,9 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     // intact until then (a wave that writes step j+1's buffer has passed the
     // barrier of step j, so all waves have finished step j-1).
     const bool late_pv = wave >= 4u;
-    bf16x8 pb_prev[G][kNH];
+    // P of the current step; late waves consume it at the start of the next
+    // step, before that step's softmax overwrites it.
+    bf16x8 pb[G][kNH];
     int bprev = 0;
     // V^T operand straight from the row-major V tile with the transposing LDS
     // read: within each 16-lane group, ds_read_b64_tr_b16 gives lane x the
@@ -267,7 +269,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         }
         const uint16_t* K = sK[b];
         const uint16_t* Vt = sV[b];
-        if (late_pv && js > js0) pv(sV[bprev], pb_prev);
+        if (late_pv && js > js0) pv(sV[bprev], pb);
 #ifdef PF_NO_COMPUTE
         if (K[tid] == 0x1234u) l_run[0] += 1.f;
         continue;
@@ -306,7 +308,6 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
                         if (pos0 + 16u * kb + (uint32_t)j > base_pos + row[g])
                             sacc[kb][g][j] = -INFINITY;
         }
-        bf16x8 pb[G][kNH];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float tm = -INFINITY;
@@ -349,16 +350,9 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
                 for (int db = 0; db < 8; ++db) acc[g][db] = acc[g][db] * ren[g];
             }
         }
-        if (late_pv) {
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int h = 0; h < kNH; ++h) pb_prev[g][h] = pb[g][h];
-        } else {
-            pv(Vt, pb);
-        }
+        if (!late_pv) pv(Vt, pb);
     }
-    if (late_pv && js0 <= js1) pv(sV[bprev], pb_prev);
+    if (late_pv && js0 <= js1) pv(sV[bprev], pb);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         l_run[g] += __shfl_xor(l_run[g], 16);
