@@ -24,9 +24,10 @@
 // step ahead), K and V row-major. Per step and column group:
 //   * S^T = K x Q^T: 4 key blocks x 4 v_mfma_f32_16x16x32_bf16 (Q^T in
 //     registers for the whole kernel);
-//   * online softmax per column over the 64 keys (lane holds 16 scores, two
-//     cross-lane xor steps), exp2 with the scale folded into one FMA, p fp32
-//     for l, bf16 (v_cvt_pk_bf16_f32) for P.V;
+//   * online softmax per column over the 64 keys (lane holds 16 scores; the
+//     column max across the 4 lane groups with two row-swap permutes), exp2
+//     with the scale folded into one FMA, p fp32 for l, bf16
+//     (v_cvt_pk_bf16_f32) for P.V;
 //   * O^T += V^T x P^T: 2 halves x 8 v_mfma_f32_16x16x32_bf16, V^T read from
 //     the row-major tile with gfx950's transposing LDS read, the contraction
 //     index permuted identically on both operands so that P^T is exactly the
