@@ -69,6 +69,45 @@ __device__ unsigned long long g_probe_t[6][8192];
 #define PROBE_T(i) do {} while (0)
 #endif
 
+// Cross-lane reductions without an LDS round trip. gfx950's row-swap
+// permutes applied to (x, x): permlane16_swap gives the 16-lane rows
+// (r0, r0, r2, r2) and (r1, r1, r3, r3), permlane32_swap the halves (lo, lo)
+// and (hi, hi). Combining the two results reduces lanes l, l^16 (then l^32)
+// with the same operands, in the same order, as xor shuffles would.
+__device__ __forceinline__ float swap16_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float swap32_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float swap16_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float swap32_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+// Max over all 64 lanes: DPP within quads, 8- and 16-lane mirrors, then the
+// row swaps (max is exact in any order).
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF,
+                                                         false)));  // quad_perm 1,0,3,2
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF,
+                                                         false)));  // quad_perm 2,3,0,1
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF,
+                                                         false)));  // row_half_mirror
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF,
+                                                         false)));  // row_mirror
+    return swap32_max(swap16_max(x));
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -508,16 +547,14 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             sc[jj] = (pos0 + (uint32_t)jj <= tend) ? v : -INFINITY;
         }
         float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        tm = fmaxf(tm, __shfl_xor(tm, 16));
-        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        tm = swap32_max(swap16_max(tm));
         const float mn = fmaxf(m_run, tm);
         const float renew = (m_run == -INFINITY) ? 0.f : __expf(m_run - mn);
         float p[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) p[jj] = __expf(sc[jj] - mn);
         float ls = (p[0] + p[1]) + (p[2] + p[3]);
-        ls += __shfl_xor(ls, 16);
-        ls += __shfl_xor(ls, 32);
+        ls = swap32_sum(swap16_sum(ls));
         l_run = l_run * renew + ls;
         m_run = mn;
         s16x4 pb;
@@ -759,8 +796,7 @@ __device__ __forceinline__ float fold_partials(const float* __restrict__ base,
         s_l[i] = ml.y;
         if (ml.y != 0.f) mx = fmaxf(mx, ml.x);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = wave_max(mx);
     if ((d & 63u) == 0u) s_red[d >> 6] = mx;
     __syncthreads();
     const float M = fmaxf(s_red[0], s_red[1]);
@@ -818,8 +854,7 @@ __device__ __forceinline__ float fold_loaded(const Loaded<NMAX>& x, uint32_t n, 
     const float m = x.m;
     const float l = d < n ? x.l : 0.f;
     float mx = (l != 0.f) ? m : -INFINITY;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = wave_max(mx);
     if ((d & 63u) == 0u) s_red[d >> 6] = mx;
     __syncthreads();
     const float M = fmaxf(s_red[0], s_red[1]);
