@@ -132,6 +132,9 @@ constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 #ifndef MCKV_KV2_MIN_BLOCKS
 #define MCKV_KV2_MIN_BLOCKS 256u
 #endif
+#ifndef MCKV_COMPACT
+#define MCKV_COMPACT 1
+#endif
 #ifndef MCKV_RING
 #define MCKV_RING 2
 #endif
@@ -737,6 +740,12 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 // grid = (ceil(NC / cpw), 2 kv heads (1 with KV2), B slots). Single-session launches pass
 // B = 1 and the direct pointers; batched launches resolve per-slot pointers
 // from device tables.
+__device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
+                                                   uint32_t NC) {
+    const uint32_t n = limit / C + 1u;
+    return n > NC ? NC : n;
+}
+
 template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2>
 __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR decode_chunk_kernel(
     const uint16_t* __restrict__ q_rows, const uint32_t* d_pos,
@@ -752,28 +761,62 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR
         g_probe_t[5][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = __builtin_amdgcn_s_getreg(6164);
     }
 #endif
-    const uint32_t slot = blockIdx.z;
+    uint32_t slot = blockIdx.z, group = blockIdx.x, limit;
+    if constexpr (BATCH && MCKV_COMPACT) {
+        // Work compaction: the (x, slot) workgroups are numbered densely over
+        // the chunk groups that exist (slot by slot, ascending), so ragged
+        // slots leave their idle workgroups at the end of the grid instead of
+        // between the working ones. Every wave derives the same mapping from
+        // all slots' limits: lane s reads slot s's limit, a DPP scan gives
+        // the running total of chunk groups, and the slot is the first one
+        // whose total exceeds this workgroup's index.
+        const uint32_t B = gridDim.z;
+        const uint32_t flat = blockIdx.x + gridDim.x * blockIdx.z;
+        {
+            const uint32_t lane = threadIdx.x & 63u;
+            uint32_t lim = 0u, cnt = 0u;
+            if (lane < B) {
+                lim = *slot_pos[lane];
+                // C is 64 * TPW in the straight-line schedule (a shift)
+                const uint32_t nv = n_valid_chunks(lim, TPW > 0u ? 64u * TPW : C, NC);
+                cnt = cpw == 1u ? nv : (nv + cpw - 1u) / cpw;
+            }
+            uint32_t incl = cnt;
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x111, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x112, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x114, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x118, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x142, 0xA, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x143, 0xC, 0xF, false);
+            slot = (uint32_t)__builtin_popcountll(
+                __builtin_amdgcn_ballot_w64(lane < B && incl <= flat));
+            if (slot < B) {
+                const uint32_t end = (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)slot);
+                const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)cnt, (int)slot);
+                group = flat - (end - c);
+                limit = (uint32_t)__builtin_amdgcn_readlane((int)lim, (int)slot);
+            }
+        }
+        if (slot >= B) return;  // past the last existing chunk group (uniform)
+    } else {
+        limit = BATCH ? *slot_pos[slot] : *d_pos;
+    }
     DecodeArgs a;
     a.q_row = q_rows + (size_t)slot * kRow;
-    a.limit = BATCH ? *slot_pos[slot] : *d_pos;
+    a.limit = limit;
     a.pt = BATCH ? slot_pt[slot] : pt;
     a.pool = BATCH ? slot_kv[slot] : pool;
     a.partials = partials + (size_t)slot * kHq * NC * kPartial;
     a.out = out + (size_t)slot * kHq * kD;
     const uint32_t kvh = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : blockIdx.y;
     decode_range_body<PH0, PAGE16, TPW, KV2>(a, layer, ly, NC, inv_freq, C, kvh,
-                                   blockIdx.x * cpw, cpw);
+                                   group * cpw, cpw);
 #ifdef MCKV_PROBE_TIMES
     __syncthreads();
     PROBE_T(3);
 #endif
 }
 
-__device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
-                                                   uint32_t NC) {
-    const uint32_t n = limit / C + 1u;
-    return n > NC ? NC : n;
-}
 
 constexpr uint32_t kMaxFold = 2048;
 

@@ -261,7 +261,7 @@ def test_phase0_matches_rope_then_attend(kvm, orc, dev, limit):
     check_vs_ref(orc, from_dev(out_b), ref, f"phase0 limit={limit}")
 
 
-def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed):
+def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed, step=37):
     import torch
     rng = np.random.default_rng(seed)
     P, L, layer = 32, 2, 1
@@ -270,7 +270,7 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed):
     perm = rng.permutation(maxp).astype(np.uint32)
     pts = [perm[s::B][:pages_per].copy() for s in range(B)]
     pool = np.full(maxp * P * 512 * L, POISON, dtype=np.uint16)
-    limits = [ctx - 37 * s for s in range(B)]
+    limits = [ctx - step * s for s in range(B)]
     for s in range(B):
         for j in range(limits[s] + (0 if ph0 else 1)):
             base = orc.kv_off(P, maxp, layer, int(pts[s][j // P]), j % P, 0, 0, 0)
@@ -345,6 +345,15 @@ def test_batch_vs_single_two_level(kvm, orc, dev, C, ph0):
     """More than 32 chunks: batched level-1 and level-2 partials and outputs
     bit-identical to single-session runs."""
     _batch_case(kvm, orc, dev, 4, C, 9000, ph0, seed=C + 1)
+
+
+@pytest.mark.parametrize("B,C", [(24, 64), (17, 256), (64, 64)])
+def test_batch_vs_single_many_slots(kvm, orc, dev, B, C):
+    """More than 16 slots (the batched kernel maps workgroups to slots with a
+    wave-wide scan instead of scalar registers) and ragged limits: outputs and
+    partials bit-identical to single-session runs, and within tolerance of
+    the oracle."""
+    _batch_case(kvm, orc, dev, B, C, 700, True, seed=B * 7 + C, step=9)
 
 
 def test_batch_vs_single_both_heads_per_workgroup(kvm, orc, dev):
