@@ -59,9 +59,10 @@ namespace {
 // Timing probe (off by default): -DMCKV_PROBE_TIMES records, per workgroup of
 // the chunk kernel, the 100 MHz real-time clock at entry (row 0), after the
 // start-up barrier (1), at the first chunk fold (2) and at exit (3), plus the
-// HW_ID (4) and XCC_ID (5) registers, read back with mckv_probe_read().
+// HW_ID (4) and XCC_ID (5) registers and the shader-clock counter at entry
+// (6) and exit (7), read back with mckv_probe_read().
 #ifdef MCKV_PROBE_TIMES
-__device__ unsigned long long g_probe_t[6][8192];
+__device__ unsigned long long g_probe_t[8][8192];
 #define PROBE_T(i) do { if (threadIdx.x == 0u) { __builtin_amdgcn_s_waitcnt(0); \
     g_probe_t[i][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = \
     __builtin_amdgcn_s_memrealtime(); } } while (0)
@@ -759,6 +760,7 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR
     if (threadIdx.x == 0u) {
         g_probe_t[4][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = __builtin_amdgcn_s_getreg(63492);
         g_probe_t[5][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = __builtin_amdgcn_s_getreg(6164);
+        g_probe_t[6][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = __builtin_amdgcn_s_memtime();
     }
 #endif
     uint32_t slot = blockIdx.z, group = blockIdx.x, limit;
@@ -814,6 +816,8 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR
 #ifdef MCKV_PROBE_TIMES
     __syncthreads();
     PROBE_T(3);
+    if (threadIdx.x == 0u)
+        g_probe_t[7][blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)] = __builtin_amdgcn_s_memtime();
 #endif
 }
 
