@@ -66,7 +66,7 @@ __device__ __forceinline__ float max_across_groups(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-constexpr uint32_t kQRows = 32;  // q rows per workgroup
+constexpr uint32_t kQRows = kThreads / 16u;  // q rows per workgroup (4 per wave)
 #ifndef PF_STEP
 #define PF_STEP 64
 #endif
@@ -77,6 +77,9 @@ static_assert(kStep == 32 || kStep == 64, "step of 32 or 64 keys");
 constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
 constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (conflict-free tr reads)
 constexpr uint32_t kBufs = 3;            // LDS K/V buffers (see the ping-pong)
+constexpr uint32_t kKeysPerPass = kThreads / 16u;  // keys one gather pass covers
+constexpr int kPass = 32 / (int)kKeysPerPass;      // passes per 32-key half
+constexpr int kStage = 2 * kNH * kPass;            // 16-byte chunks per thread and step
 
 template <bool PAGE_STEP>
 __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
@@ -140,12 +143,17 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
 
     // Cooperative gather: per 32-key half, thread tid moves the 16-byte K and
     // V chunks of key tid/16, dims 8*(tid%16) (16 threads per 256-byte row).
-    uint4 stage[2 * kNH];  // [K chunks of each half, then V chunks]
+    uint4 stage[kStage];  // [K chunks of each half and pass, then V chunks]
     const uint32_t kkey = tid >> 4, kdb = tid & 15u;
+    // key (within the step) and K/V half of stage slot r
+    auto key_of = [&](int r) {
+        const int rem = r % (kNH * kPass);
+        return 32u * (uint32_t)(rem / kPass) + kKeysPerPass * (uint32_t)(rem % kPass) + kkey;
+    };
     // Page ids are fetched one step ahead of the K/V loads that use them, so
     // a gather waits for one memory latency, not two. With P >= kStep a step lies
     // in one page and its id is read through the scalar path.
-    auto page_ids = [&](uint32_t js, uint32_t (&pg)[2 * kNH]) {
+    auto page_ids = [&](uint32_t js, uint32_t (&pg)[kStage]) {
         if constexpr (PAGE_STEP) {
             const uint32_t pos = js * kStep;
             const uint32_t id = pos <= key_end
@@ -153,16 +161,16 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
                                           [__builtin_amdgcn_readfirstlane(pos >> ly.log2p)]
                                     : 0u;
 #pragma unroll
-            for (int r = 0; r < 2 * kNH; ++r) pg[r] = id;
+            for (int r = 0; r < kStage; ++r) pg[r] = id;
         } else {
 #pragma unroll
-            for (int r = 0; r < 2 * kNH; ++r) {
-                const uint32_t pos = js * kStep + 32u * (r % kNH) + kkey;
+            for (int r = 0; r < kStage; ++r) {
+                const uint32_t pos = js * kStep + key_of(r);
                 pg[r] = pos <= key_end ? pt[pos >> ly.log2p] : 0u;
             }
         }
     };
-    auto gather = [&](uint32_t js, const uint32_t (&pg)[2 * kNH]) {
+    auto gather = [&](uint32_t js, const uint32_t (&pg)[kStage]) {
         if constexpr (PAGE_STEP) {
             // The step lies in one page: scalar page base, 32-bit lane offsets,
             // and no per-lane range test unless the step passes key_end.
@@ -170,10 +178,10 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
             const uint32_t step0 = js * kStep;
             const bool full = step0 + kStep - 1u <= key_end;  // wave-uniform
 #pragma unroll
-            for (int r = 0; r < 2 * kNH; ++r) {
-                const uint32_t key = 32u * (r % kNH) + kkey;
+            for (int r = 0; r < kStage; ++r) {
+                const uint32_t key = key_of(r);
                 const uint32_t off = ((step0 + key) & ly.pmask) * kSlotElems +
-                                     (r >= kNH ? 256u : 0u) + kvh * kD + kdb * 8u;
+                                     (r >= kNH * kPass ? 256u : 0u) + kvh * kD + kdb * 8u;
                 if (full) {
                     stage[r] = *reinterpret_cast<const uint4*>(pbase + off);
                 } else {
@@ -185,9 +193,9 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
             return;
         }
 #pragma unroll
-        for (int r = 0; r < 2 * kNH; ++r) {
-            const bool isv = r >= kNH;
-            const uint32_t key = 32u * (r % kNH) + kkey;
+        for (int r = 0; r < kStage; ++r) {
+            const bool isv = r >= kNH * kPass;
+            const uint32_t key = key_of(r);
             const uint32_t dblk = kdb;
             const uint32_t pos = js * kStep + key;
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
@@ -205,10 +213,10 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     };
     auto put = [&](int b) {
 #pragma unroll
-        for (int h = 0; h < kNH; ++h) {
-            *reinterpret_cast<uint4*>(&sK[b][(32u * h + kkey) * kKPitch + kdb * 8u]) = stage[h];
-            *reinterpret_cast<uint4*>(&sV[b][(32u * h + kkey) * kVPitch + kdb * 8u]) =
-                stage[kNH + h];
+        for (int r = 0; r < kNH * kPass; ++r) {
+            const uint32_t key = key_of(r);
+            *reinterpret_cast<uint4*>(&sK[b][key * kKPitch + kdb * 8u]) = stage[r];
+            *reinterpret_cast<uint4*>(&sV[b][key * kVPitch + kdb * 8u]) = stage[kNH * kPass + r];
         }
     };
 
@@ -218,7 +226,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     // summed across the 4 lane groups at the end.
     constexpr float kC = kScoreScale * 1.4426950408889634f;
     constexpr float kMoveSlack = 8.f / kC;  // 8 in log2 units, in raw score units
-    uint32_t pgn[2 * kNH] = {};
+    uint32_t pgn[kStage] = {};
     if (js0 <= js1) {
         page_ids(js0, pgn);
         gather(js0, pgn);
