@@ -226,6 +226,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     // summed across the 4 lane groups at the end.
     constexpr float kC = kScoreScale * 1.4426950408889634f;
     constexpr float kMoveSlack = 8.f / kC;  // 8 in log2 units, in raw score units
+    constexpr float kSumCap = 256.f;        // lane sum of p that still bounds p by 2^8
     uint32_t pgn[kStage] = {};
     if (js0 <= js1) {
         page_ids(js0, pgn);
@@ -319,6 +320,26 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
+            // Fast path: once every column has a reference, p is computed
+            // against it directly; a lane sum of at most kSumCap bounds every
+            // p by 2^8 as the max test below would, so the max is needed only
+            // when the sum says the reference may have to move (wave-uniform).
+            if (__builtin_amdgcn_ballot_w64(m_run[g] == -INFINITY) == 0u) {
+                float ls = 0.f;
+#pragma unroll
+                for (int kb = 0; kb < kNKB; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float p =
+                            __builtin_amdgcn_exp2f(fmaf(sacc[kb][g][j], kC, nmc[g]));
+                        ls += p;
+                        pb[g][kb >> 1][4 * (kb & 1) + j] = (__bf16)p;
+                    }
+                if (__builtin_amdgcn_ballot_w64(ls > kSumCap) == 0u) {
+                    l_run[g] += ls;
+                    continue;
+                }
+            }
             float tm = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < kNKB; ++kb)
