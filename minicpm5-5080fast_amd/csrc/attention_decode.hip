@@ -1058,7 +1058,7 @@ mc_status_t launch_chunks(const uint16_t* q, const uint32_t* d_pos,
     const dim3 grid(nx, kv2 ? 1u : kHkv, B);
     const dim3 block(kv2 ? kHkv * kThreads : kThreads);
 #define MCKV_LAUNCH_CHUNK_KV(PH, PG, TP, KV)                                                 \
-    hipLaunchKernelGGL((decode_chunk_kernel<PH, BATCH, PG, TP, KV>), grid, block, 0, st,     \
+    hipLaunchKernelGGL((decode_chunk_kernel<PH, BATCH, PG, TP, KV && !BATCH>), grid, block, 0, st, \
                        q, d_pos, slot_pos, layer, pt, slot_pt, pool, slot_kv, ly, partials,  \
                        NC, out, inv_freq, C, cpw)
 #define MCKV_LAUNCH_CHUNK(PH, PG, TP) MCKV_LAUNCH_CHUNK_KV(PH, PG, TP, false)
