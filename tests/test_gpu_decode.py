@@ -122,7 +122,7 @@ def test_decode_pos0_equals_v0(kvm, orc, dev):
     assert np.array_equal(got.reshape(16, 128), np.repeat(v, 8, axis=0))
 
 
-@pytest.mark.parametrize("C", [64, 128, 256])
+@pytest.mark.parametrize("C", [64, 128, 256, 512])
 @pytest.mark.parametrize("P", [32, 64])
 def test_decode_chunk_tiers(kvm, orc, dev, C, P):
     rng = np.random.default_rng(C * 7 + P)
@@ -347,7 +347,7 @@ def test_batch_vs_single_two_level(kvm, orc, dev, C, ph0):
     _batch_case(kvm, orc, dev, 4, C, 9000, ph0, seed=C + 1)
 
 
-@pytest.mark.parametrize("B,C", [(24, 64), (17, 256), (64, 64)])
+@pytest.mark.parametrize("B,C", [(24, 64), (17, 256), (64, 64), (9, 512)])
 def test_batch_vs_single_many_slots(kvm, orc, dev, B, C):
     """More than 16 slots (the batched kernel maps workgroups to slots with a
     wave-wide scan instead of scalar registers) and ragged limits: outputs and
@@ -364,7 +364,8 @@ def test_batch_vs_single_both_heads_per_workgroup(kvm, orc, dev):
 
 
 @pytest.mark.parametrize("ctx,C,ph0", [(40000, 64, True), (131072, 256, True),
-                                       (70001, 256, False)])
+                                       (70001, 256, False), (131072, 512, True),
+                                       (90001, 512, False)])
 def test_decode_long_multichunk_blocks(kvm, orc, dev, ctx, C, ph0):
     """Long contexts where one workgroup streams several chunks (2x512+
     chunk units), P = 64, permuted pages; phase0 appends position ctx-1."""
