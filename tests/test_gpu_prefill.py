@@ -16,7 +16,7 @@ POISON = 0xDCBA
 
 
 def run_prefill(kvm, orc, dev, T, base, S, P=32, seed=0, sentinel=False, check=True,
-                abs_check=True):
+                abs_check=True, kgrow=0.0):
     import torch
     rng = np.random.default_rng(seed)
     ctx = base + T
@@ -27,6 +27,9 @@ def run_prefill(kvm, orc, dev, T, base, S, P=32, seed=0, sentinel=False, check=T
     for j in range(ctx):
         off = orc.kv_off(P, maxp, layer, int(pt[j // P]), j % P, 0, 0, 0)
         pool[off:off + 512] = randn_bf16(rng, 512, 0.6)
+        if kgrow:  # K magnitude growing with position: the running max keeps moving
+            k = orc.bf16_to_f32(pool[off:off + 256]) * np.float32(1.0 + kgrow * j / ctx)
+            pool[off:off + 256] = orc.f32_to_bf16(k.astype(np.float32))
         if sentinel and j >= base + 40:  # V = 40 for future positions
             pool[off + 256:off + 512] = orc.f32_to_bf16(np.float32([40.0]))[0]
     q = randn_bf16(rng, T * 2560, 1.0).reshape(T, 2560)
@@ -89,3 +92,11 @@ def test_prefill_long_chunk(kvm, orc, dev):
     """2048 rows over a 300-token prefix: many steps per tile, reference max
     moving late in long rows."""
     run_prefill(kvm, orc, dev, 2048, 300, 1, P=64, seed=21)
+
+
+@pytest.mark.parametrize("T,base,S", [(512, 0, 1), (300, 40, 4), (96, 8448, 1)])
+def test_prefill_growing_scores(kvm, orc, dev, T, base, S):
+    """Keys whose magnitude grows tenfold along the context: the softmax
+    reference moves many times mid-row (accumulator rescales) and lane sums
+    overflow the fast-path bound, so both softmax paths run."""
+    run_prefill(kvm, orc, dev, T, base, S, P=64, seed=T + S, kgrow=9.0)
