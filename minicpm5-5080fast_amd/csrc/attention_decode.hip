@@ -774,14 +774,18 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR
         // whose total exceeds this workgroup's index.
         const uint32_t B = gridDim.z;
         const uint32_t flat = blockIdx.x + gridDim.x * blockIdx.z;
+        const uint32_t Cc = TPW > 0u ? 64u * TPW : C;  // 64 * TPW: a shift
+        const bool cpw_pow2 = (cpw & (cpw - 1u)) == 0u;
+        const uint32_t cpw_log2 = (uint32_t)__builtin_ctz(cpw);
+        auto groups = [&](uint32_t nv) {
+            return cpw_pow2 ? (nv + cpw - 1u) >> cpw_log2 : (nv + cpw - 1u) / cpw;
+        };
         {
             const uint32_t lane = threadIdx.x & 63u;
             uint32_t lim = 0u, cnt = 0u;
             if (lane < B) {
                 lim = *slot_pos[lane];
-                // C is 64 * TPW in the straight-line schedule (a shift)
-                const uint32_t nv = n_valid_chunks(lim, TPW > 0u ? 64u * TPW : C, NC);
-                cnt = cpw == 1u ? nv : (nv + cpw - 1u) / cpw;
+                cnt = groups(n_valid_chunks(lim, Cc, NC));
             }
             uint32_t incl = cnt;
             incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x111, 0xF, 0xF, false);
