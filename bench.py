@@ -9,7 +9,7 @@ the headline workload C4 (one session, 131072 cached tokens in 2048 pages of
 second over the whole timed region (inputs resident in HBM); the other
 configurations are reported under "configs".
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,c5,pf]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,c5,pf,alloc]
 """
 from __future__ import annotations
 
@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c4,c3,c1,c2,c5,pf")
+    ap.add_argument("--configs", default="c4,c3,c1,c2,c5,pf,alloc")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (eager launches)")
@@ -456,6 +456,35 @@ def cpu_baseline(seconds: float):
     }
 
 
+def bench_alloc(kvm):
+    """Host page allocator (reference kv_cache.cpp:8-91 semantics, shared-pool
+    form): 8 sessions grown to 131072 tokens of 64-token pages in one pool,
+    then released; per-page cost of the C++ allocator (one ensure call per
+    session, no page-table upload) and of the oracle's Python model on a
+    one-session sample (the CPU port baseline)."""
+    import oracle
+    P, B, ctx = 64, 8, 131072
+    per = ctx // P
+    maxp = B * per
+    pool = kvm.SharedPagePool(maxp, P, B)
+    t0 = time.perf_counter()
+    for s in range(B):
+        pool.ensure(s, ctx)
+    t1 = time.perf_counter()
+    for s in range(B):
+        pool.release(s)
+    t2 = time.perf_counter()
+    pool.close()
+    model = oracle.SharedPoolModel(maxp, P, B)
+    t3 = time.perf_counter()
+    model.ensure(0, ctx)
+    t4 = time.perf_counter()
+    return {"pages": B * per, "ns_per_page_acquire": (t1 - t0) / (B * per) * 1e9,
+            "ns_per_page_release": (t2 - t1) / (B * per) * 1e9,
+            "oracle_ns_per_page_acquire": (t4 - t3) / per * 1e9,
+            "oracle_sample": f"1 session x {per} pages, Python model"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -499,6 +528,9 @@ def main():
         res["c5_churn"] = bench_churn(kvm, torch, dev, timer)
         log(res["c5_churn"])
         torch.cuda.empty_cache()
+    if "alloc" in cfgs:
+        res["alloc_host"] = bench_alloc(kvm)
+        log(res["alloc_host"])
     if "pf" in cfgs:
         for base in (0, 8448):
             log(f"prefill attention 8448 tokens at base {base} ...")
