@@ -36,7 +36,7 @@
 //   * QK: S^T[16 pos][16 heads] = K (A operand) x Q^T (B operand, preloaded;
 //     heads 8..15 are zero padding) with four v_mfma_f32_16x16x32_bf16.
 //   * The D layout gives each lane 4 positions of one head; the batch max/sum
-//     need two cross-lane xor steps (16, 32).
+//     combine the 4 lane groups with two row-swap permutes (16, 32).
 //   * P.V: O^T += V^T x P^T (v_mfma_f32_16x16x16bf16_1k). The V^T A operand
 //     comes from the LDS tile through the transposing read ds_read_b64_tr_b16;
 //     P^T (B operand) is the softmax output already in the right lanes. (The
