@@ -23,7 +23,10 @@
 //     the fresh values; q is rotated on the fly (LDS) and never written back.
 //
 // MI355X design (one 256-thread workgroup = 4 wave64 per (slot, kv head,
-// range of chunks)). Each wave walks 16-position tiles t = wave, wave+4, ...
+// range of chunks); single-session 256/512-position tiers with at least 256
+// workgroups put both KV heads in one 512-thread workgroup, and batched
+// launches number their workgroups densely over the slots' existing chunk
+// groups). Each wave walks 16-position tiles t = wave, wave+4, ...
 // of each chunk and keeps its own online-softmax state for all 8 query heads
 // of the KV head; the 4 wave states are folded through LDS per chunk. The next
 // tile's loads are in flight while the current tile computes.
