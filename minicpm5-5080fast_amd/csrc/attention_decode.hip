@@ -461,12 +461,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     if (PH0) {
         // cos/sin of pair p = tid % 64 (every wave evaluates the same 64)
         float c, sn;
-#ifdef MCKV_PROBE_NO_SINCOS
-        c = 1.f + (float)limit * invf * 1e-30f;
-        sn = 0.f;
-#else
         rope_sincos((float)limit * invf, &c, &sn);
-#endif
         const uint32_t p = tid & 63u;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
@@ -528,15 +523,6 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // Accumulates the tile starting at position `tstart` (rows after `tend`
     // masked) into the current chunk state.
     auto accumulate = [&](const Tile& T, uint32_t tstart, uint32_t tend) {
-#ifdef MCKV_PROBE_NO_COMPUTE
-        {
-            uint32_t x = 0;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) x ^= T.k[m].x ^ T.k[m].w ^ T.v[m].y ^ T.v[m].z;
-            l_run += (float)(x & 1u);
-            return;
-        }
-#endif
         // S^T = K x Q^T
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

@@ -203,11 +203,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
             const uint32_t dblk = kdb;
             const uint32_t pos = js * kStep + key;
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
-#ifdef PF_NO_GATHER
-            if (pos == 0xFFFFFFFFu) {
-#else
             if (pos <= key_end) {
-#endif
                 v = *reinterpret_cast<const uint4*>(
                     pool + token_base(ly, layer, pg[r], pos & ly.pmask) + (isv ? 256u : 0u) +
                     kvh * kD + dblk * 8u);
@@ -290,10 +286,6 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
         const uint16_t* K = sK[b];
         const uint16_t* Vt = sV[b];
         if (late_pv && js > js0) pv(sV[bprev], pb);
-#ifdef PF_NO_COMPUTE
-        if (K[tid] == 0x1234u) l_run[0] += 1.f;
-        continue;
-#endif
         // S^T blocks: key block kb (keys 16kb + row), lane col = query column.
         f32x4 sacc[kNKB][G];
         {
