@@ -363,15 +363,15 @@ def test_batch_vs_single_both_heads_per_workgroup(kvm, orc, dev):
     _batch_case(kvm, orc, dev, 2, 256, 131000, True, seed=0x2C4)
 
 
-@pytest.mark.parametrize("ctx,C,ph0", [(40000, 64, True), (131072, 256, True),
-                                       (70001, 256, False), (131072, 512, True),
-                                       (90001, 512, False)])
-def test_decode_long_multichunk_blocks(kvm, orc, dev, ctx, C, ph0):
+@pytest.mark.parametrize("ctx,C,ph0,P", [(40000, 64, True, 64), (131072, 256, True, 64),
+                                         (70001, 256, False, 64), (131072, 512, True, 64),
+                                         (90001, 512, False, 64), (131072, 256, True, 16)])
+def test_decode_long_multichunk_blocks(kvm, orc, dev, ctx, C, ph0, P):
     """Long contexts where one workgroup streams several chunks (2x512+
-    chunk units), P = 64, permuted pages; phase0 appends position ctx-1."""
+    chunk units), permuted pages of P tokens; phase0 appends position ctx-1."""
     import torch
-    rng = np.random.default_rng(ctx)
-    P, L, layer = 64, 2, 1
+    rng = np.random.default_rng(ctx + P)
+    L, layer = 2, 1
     maxp = -(-ctx // P) + 2
     pt = rng.permutation(maxp).astype(np.uint32)
     lay = kvm.KvLayout(maxp, P, L)
