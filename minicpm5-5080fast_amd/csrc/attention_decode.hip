@@ -776,6 +776,8 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads) MCKV_CHUNK_ATTR
                 lim = *slot_pos[lane];
                 cnt = groups(n_valid_chunks(lim, Cc, NC));
             }
+            // inclusive scan over the 64 lanes: row_shr 1, 2, 4, 8 within each
+            // 16-lane row, then row_bcast 15 (into rows 1, 3) and 31 (rows 2, 3)
             uint32_t incl = cnt;
             incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x111, 0xF, 0xF, false);
             incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x112, 0xF, 0xF, false);
