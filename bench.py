@@ -539,6 +539,15 @@ def main():
             res[f"prefill_attn_8448_base{base}"] = r
             log(r)
             torch.cuda.empty_cache()
+        # the reference's published kernel-level prefill points (RTX 5080,
+        # kernels.h:544-547): T=2048 0.309 ms, T=8192 3.222 ms per layer
+        for T, ref_ms in ((2048, 0.309), (8192, 3.222)):
+            log(f"prefill attention {T} tokens at base 0 ...")
+            r = bench_prefill(kvm, torch, dev, timer, T, 0, max(2, args.steps // 4), 1)
+            r["reference_rtx5080_ms_per_layer"] = ref_ms
+            res[f"prefill_attn_{T}_base0"] = r
+            log(r)
+            torch.cuda.empty_cache()
 
     if args.calib:
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
