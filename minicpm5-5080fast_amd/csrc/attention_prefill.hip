@@ -17,6 +17,8 @@
 //
 // MI355X design: one 512-thread workgroup (8 wave64, 2 per SIMD) per (kv
 // head, 32-row q tile, key split); heavy (late) q tiles are launched first.
+// Launches with fewer than 512 such workgroups use 256-thread workgroups of
+// 16 rows instead (4 waves, two LDS buffers), so small T still fills the CUs.
 // The 32 rows x 8 query heads of a KV head are 256 query vectors: wave w owns
 // two 16-column groups, group g holding rows 4w + 2g + {0, 1} x heads 0..7.
 // Keys stream in 64-position steps gathered through the page table into LDS
@@ -49,7 +51,18 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kThreads = 512;
+#ifndef MC_PF_SMALL_BELOW
+#define MC_PF_SMALL_BELOW 512u  // 32-row workgroups (2 per CU) below which 16-row tiles are used
+#endif
+// Workgroup shape: 512 threads (8 waves, 32 q rows) by default; SMALL = 256
+// threads (4 waves, 16 q rows, two LDS buffers, no ping-pong) doubles the
+// workgroup count for chunks too short to fill the 256 CUs with 32-row tiles.
+template <bool SMALL>
+struct PfShape {
+    static constexpr uint32_t kThreads = SMALL ? 256u : 512u;
+    static constexpr uint32_t kQRows = kThreads / 16u;  // q rows per workgroup (4 per wave)
+    static constexpr uint32_t kBufs = SMALL ? 2u : 3u;  // LDS K/V buffers (see the ping-pong)
+};
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) {
     return __builtin_bit_cast(bf16x8, u);
@@ -66,7 +79,6 @@ __device__ __forceinline__ float max_across_groups(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-constexpr uint32_t kQRows = kThreads / 16u;  // q rows per workgroup (4 per wave)
 #ifndef PF_STEP
 #define PF_STEP 64
 #endif
@@ -76,21 +88,24 @@ constexpr int kNH = kStep / 32;      // 32-key halves per step (one PV MFMA each
 static_assert(kStep == 32 || kStep == 64, "step of 32 or 64 keys");
 constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
 constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (conflict-free tr reads)
-constexpr uint32_t kBufs = 3;            // LDS K/V buffers (see the ping-pong)
 // LDS operand reads issued this many MFMA blocks ahead of their use (software
 // pipelining written out in the source; 6-16 measured alike, 2% faster than
 // reading each operand right before its MFMAs).
 constexpr int kOperandAhead = 8;
-constexpr uint32_t kKeysPerPass = kThreads / 16u;  // keys one gather pass covers
-constexpr int kPass = 32 / (int)kKeysPerPass;      // passes per 32-key half
-constexpr int kStage = 2 * kNH * kPass;            // 16-byte chunks per thread and step
 
-template <bool PAGE_STEP>
-__global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
+template <bool PAGE_STEP, bool SMALL>
+__global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
+    __attribute__((amdgpu_waves_per_eu(2))) prefill_attn_kernel(
     const uint16_t* __restrict__ q_rows, uint32_t T,
     const uint32_t* __restrict__ d_base_pos, uint32_t layer,
     const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
     uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S) {
+    constexpr uint32_t kThreads = PfShape<SMALL>::kThreads;
+    constexpr uint32_t kQRows = PfShape<SMALL>::kQRows;
+    constexpr uint32_t kBufs = PfShape<SMALL>::kBufs;
+    constexpr uint32_t kKeysPerPass = kThreads / 16u;  // keys one gather pass covers
+    constexpr int kPass = 32 / (int)kKeysPerPass;      // passes per 32-key half
+    constexpr int kStage = 2 * kNH * kPass;            // 16-byte chunks per thread and step
     __shared__ __align__(16) uint16_t sK[kBufs][kStep * kKPitch];
     __shared__ __align__(16) uint16_t sV[kBufs][kStep * kVPitch];
 
@@ -238,7 +253,7 @@ __global__ void __launch_bounds__(kThreads) prefill_attn_kernel(
     // while the other runs the softmax. Three LDS buffers keep step j's V
     // intact until then (a wave that writes step j+1's buffer has passed the
     // barrier of step j, so all waves have finished step j-1).
-    const bool late_pv = wave >= 4u;
+    const bool late_pv = !SMALL && wave >= 4u;
     // P of the current step; late waves consume it at the start of the next
     // step, before that step's softmax overwrites it.
     bf16x8 pb[G][kNH];
@@ -474,16 +489,27 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
                   tokens, S_kv, (void*)d_partials);
         return MC_E_INVALID_ARGUMENT;
     }
-    const uint32_t ntq = (tokens + kQRows - 1u) / kQRows;
     hipStream_t st = (hipStream_t)stream;
-    if ((1u << ly.log2p) >= kStep)
-        hipLaunchKernelGGL(prefill_attn_kernel<true>, dim3(kHkv * ntq * S_kv), dim3(kThreads),
-                           0, st, d_q_rows, tokens, d_base_pos, layer, d_page_table,
-                           d_kv_pool, ly, d_out, d_partials, S_kv);
-    else
-        hipLaunchKernelGGL(prefill_attn_kernel<false>, dim3(kHkv * ntq * S_kv),
-                           dim3(kThreads), 0, st, d_q_rows, tokens, d_base_pos, layer,
-                           d_page_table, d_kv_pool, ly, d_out, d_partials, S_kv);
+    // 16-row tiles when 32-row tiles would give fewer than two workgroups per
+    // CU (measured: T=2048 67 -> 60 us, T=4096 125 -> 118 us); both shapes
+    // compute every row the same way.
+    const uint32_t ntq32 = (tokens + PfShape<false>::kQRows - 1u) / PfShape<false>::kQRows;
+    const bool small = kHkv * ntq32 * S_kv < MC_PF_SMALL_BELOW;
+#define MC_PF_LAUNCH(PG, SM)                                                                 \
+    hipLaunchKernelGGL((prefill_attn_kernel<PG, SM>),                                        \
+                       dim3(kHkv * ((tokens + PfShape<SM>::kQRows - 1u) / PfShape<SM>::kQRows) * \
+                            S_kv),                                                           \
+                       dim3(PfShape<SM>::kThreads), 0, st, d_q_rows, tokens, d_base_pos, layer, \
+                       d_page_table, d_kv_pool, ly, d_out, d_partials, S_kv)
+    const bool page_step = (1u << ly.log2p) >= kStep;
+    if (page_step) {
+        if (small) MC_PF_LAUNCH(true, true);
+        else MC_PF_LAUNCH(true, false);
+    } else {
+        if (small) MC_PF_LAUNCH(false, true);
+        else MC_PF_LAUNCH(false, false);
+    }
+#undef MC_PF_LAUNCH
     if (S_kv > 1u)
         hipLaunchKernelGGL(prefill_merge_kernel, dim3(tokens * 16u), dim3(128), 0, st,
                            d_partials, S_kv, tokens, d_out);
