@@ -965,14 +965,10 @@ __global__ void __launch_bounds__(128) merge_b_kernel(
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
     Loaded<kSplit2> x;
     const float* base = partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial;
-    bool active;
-    if constexpr (BATCH) {
-        active = n_valid_chunks(*slot_pos[slot], C, NC) > 1u;
-        load_partials<kSplit2>(base, kPartial, active ? kSplit2 : 1u, x);
-    } else {
-        load_partials<kSplit2>(base, kPartial, kSplit2, x);
-        active = n_valid_chunks(*d_pos, C, NC) > 1u;
-    }
+    // The 32 rows lie inside the caller's buffer for every slot, so they are
+    // loaded before the limit (an inactive slot's rows are never used).
+    load_partials<kSplit2>(base, kPartial, kSplit2, x);
+    const bool active = n_valid_chunks(BATCH ? *slot_pos[slot] : *d_pos, C, NC) > 1u;
     float M, L;
     const float A = fold_loaded<kSplit2>(x, kSplit2, M, L);
     if (active)
@@ -996,6 +992,7 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
         Loaded<NMAX> x;
         uint32_t nv;
         if constexpr (BATCH) {
+            // loads after the limit: measured faster for the batched launch
             nv = n_valid_chunks(*slot_pos[slot], C, NC);
             load_partials<NMAX>(base, kPartial, nv, x);
         } else {
