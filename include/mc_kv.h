@@ -224,6 +224,14 @@ mc_status_t mc_debug_session_info(mc_session_t session, uint32_t* seq_len,
 /* Copies the first n token ids of the device sequence (n <= seq_len). */
 mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n);
 
+/* Prefill workgroup shape: launches with fewer than `workgroups` 32-row
+ * workgroups use 16-row ones (bit-identical results for S_kv = 1; with key
+ * splits the split boundaries follow each tile's last row). Default 512;
+ * 0 keeps 32-row tiles always, 0xFFFFFFFF selects 16-row tiles always. The
+ * previous value is stored to *previous when that is not NULL. Process-wide;
+ * for tests that run both shapes on the same inputs. */
+mc_status_t mc_kv_debug_prefill_small_below(uint32_t workgroups, uint32_t* previous);
+
 /* Library build identity, e.g. "minicpm-kv gfx950". */
 const char* mc_kv_build_info(void);
 

@@ -39,6 +39,7 @@
 // and differ only in rounding.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 
 #include "error.h"
@@ -52,11 +53,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #ifndef MC_PF_SMALL_BELOW
-#define MC_PF_SMALL_BELOW 512u  // 32-row workgroups (2 per CU) below which 16-row tiles are used
+#define MC_PF_SMALL_BELOW 512u  // default: 32-row workgroups (2 per CU) below which 16-row tiles are used
 #endif
 // Workgroup shape: 512 threads (8 waves, 32 q rows) by default; SMALL = 256
 // threads (4 waves, 16 q rows, two LDS buffers, no ping-pong) doubles the
 // workgroup count for chunks too short to fill the 256 CUs with 32-row tiles.
+// Shape threshold in force (a debug hook sets it; see mc_kv.h).
+std::atomic<uint32_t> g_small_below{MC_PF_SMALL_BELOW};
+
 template <bool SMALL>
 struct PfShape {
     static constexpr uint32_t kThreads = SMALL ? 256u : 512u;
@@ -472,6 +476,13 @@ __global__ void __launch_bounds__(128) prefill_merge_kernel(
 
 using namespace mckv;
 
+extern "C" mc_status_t mc_kv_debug_prefill_small_below(uint32_t workgroups,
+                                                       uint32_t* previous) {
+    const uint32_t prev = mckv::g_small_below.exchange(workgroups);
+    if (previous != nullptr) *previous = prev;
+    return MC_OK;
+}
+
 extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_t tokens,
                                                const uint32_t* d_base_pos, uint32_t layer,
                                                const uint32_t* d_page_table,
@@ -492,9 +503,10 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
     hipStream_t st = (hipStream_t)stream;
     // 16-row tiles when 32-row tiles would give fewer than two workgroups per
     // CU (measured: T=2048 67 -> 60 us, T=4096 125 -> 118 us); both shapes
-    // compute every row the same way.
+    // compute every row the same way (with S_kv > 1 the split boundaries
+    // follow each tile's last row, so they differ between the shapes).
     const uint32_t ntq32 = (tokens + PfShape<false>::kQRows - 1u) / PfShape<false>::kQRows;
-    const bool small = kHkv * ntq32 * S_kv < MC_PF_SMALL_BELOW;
+    const bool small = kHkv * ntq32 * S_kv < g_small_below.load(std::memory_order_relaxed);
 #define MC_PF_LAUNCH(PG, SM)                                                                 \
     hipLaunchKernelGGL((prefill_attn_kernel<PG, SM>),                                        \
                        dim3(kHkv * ((tokens + PfShape<SM>::kQRows - 1u) / PfShape<SM>::kQRows) * \

@@ -142,6 +142,16 @@ def launch_attn_prefill_flash(d_q_rows, tokens, d_base_pos, layer, d_page_table,
                                         _stream(stream)), "launch_attn_prefill_flash")
 
 
+def debug_prefill_small_below(workgroups: int) -> int:
+    """Sets the prefill shape threshold (32-row workgroup count below which
+    16-row workgroups are used; 0 = never, 0xFFFFFFFF = always) and returns
+    the previous one. Debug hook, no reference counterpart."""
+    prev = C.c_uint32(0)
+    check(lib().mc_kv_debug_prefill_small_below(workgroups, C.byref(prev)),
+          "debug_prefill_small_below")
+    return prev.value
+
+
 def launch_decode_advance(d_seq, d_next_token, d_seq_len, stream=None) -> None:
     check(lib().mc_kv_decode_advance(_ptr(d_seq), _ptr(d_next_token), _ptr(d_seq_len),
                                      _stream(stream)), "launch_decode_advance")

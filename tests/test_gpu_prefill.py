@@ -100,3 +100,26 @@ def test_prefill_growing_scores(kvm, orc, dev, T, base, S):
     reference moves many times mid-row (accumulator rescales) and lane sums
     overflow the fast-path bound, so both softmax paths run."""
     run_prefill(kvm, orc, dev, T, base, S, P=64, seed=T + S, kgrow=9.0)
+
+
+@pytest.mark.parametrize("T,base,S,P,kgrow", [(80, 13, 1, 32, 0.0), (1024, 7, 8, 32, 0.0),
+                                              (300, 40, 4, 64, 9.0), (150, 29, 1, 8, 0.0),
+                                              (96, 8448, 1, 64, 0.0), (1, 0, 1, 32, 0.0),
+                                              (512, 0, 1, 64, 9.0)])
+def test_prefill_both_shapes(kvm, orc, dev, T, base, S, P, kgrow):
+    """The 32-row workgroups (8 waves, ping-pong P.V) and the 16-row ones
+    (4 waves) compute every row the same way: without key splits the outputs
+    are bit-identical. With S > 1 a tile's split boundaries follow its last
+    row, so the partials group differently and both shapes are held to the
+    oracle tolerance instead. The launch picks the shape from the workgroup
+    count; the debug hook forces each one here."""
+    prev = kvm.debug_prefill_small_below(0)
+    try:
+        wide = run_prefill(kvm, orc, dev, T, base, S, P=P, seed=T + S, kgrow=kgrow)
+        kvm.debug_prefill_small_below(0xFFFFFFFF)
+        narrow = run_prefill(kvm, orc, dev, T, base, S, P=P, seed=T + S, kgrow=kgrow,
+                             check=S > 1)
+    finally:
+        kvm.debug_prefill_small_below(prev)
+    if S == 1:
+        assert np.array_equal(wide, narrow), "32-row and 16-row shapes differ"
