@@ -125,11 +125,9 @@ constexpr uint32_t kPageCache = 128;  // page ids staged in LDS per block
 #endif
 constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 
-// Tuning knobs (compile-time): tiles in flight per wave beyond the one being
-// computed, forced waves per SIMD (0 = compiler choice), streaming loads.
-#ifndef MCKV_PREFETCH
-#define MCKV_PREFETCH 1
-#endif
+// Tuning knobs (compile-time): forced waves per SIMD (0 = compiler choice),
+// the smallest grid that takes two-head workgroups, batched work compaction,
+// K/V tiles in the per-wave ring, and the load layout per chunk tier.
 #ifndef MCKV_WAVES_PER_EU
 #define MCKV_WAVES_PER_EU 2
 #endif
@@ -157,18 +155,8 @@ constexpr uint32_t kFoldSlots = MCKV_FOLD_SLOTS;  // chunks stashed per fold
 #ifndef MCKV_V_ROW_MIN_TPW
 #define MCKV_V_ROW_MIN_TPW 2u  // smallest tiles-per-wave tier using V row loads
 #endif
-#ifndef MCKV_NT_LOADS
-#define MCKV_NT_LOADS 0
-#endif
-
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
-#if MCKV_NT_LOADS
-    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-    return __builtin_bit_cast(uint4, __builtin_nontemporal_load(
-                                         reinterpret_cast<const u32x4*>(p)));
-#else
     return *reinterpret_cast<const uint4*>(p);
-#endif
 }
 
 struct Tile {
