@@ -232,6 +232,13 @@ mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n)
  * for tests that run both shapes on the same inputs. */
 mc_status_t mc_kv_debug_prefill_small_below(uint32_t workgroups, uint32_t* previous);
 
+/* Prefill job packing: with key splits off, two to three 32-row jobs per CU
+ * and a prefix of at least T/4, one workgroup per CU runs a fixed 2-3 job
+ * packing instead of greedy dispatch (identical results). enable = 0 turns it
+ * off (default on). The previous setting is stored to *previous when that is
+ * not NULL. Process-wide; for tests that compare both schedules. */
+mc_status_t mc_kv_debug_prefill_packing(uint32_t enable, uint32_t* previous);
+
 /* Library build identity, e.g. "minicpm-kv gfx950". */
 const char* mc_kv_build_info(void);
 

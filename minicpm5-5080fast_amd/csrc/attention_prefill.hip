@@ -58,8 +58,26 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Workgroup shape: 512 threads (8 waves, 32 q rows) by default; SMALL = 256
 // threads (4 waves, 16 q rows, two LDS buffers, no ping-pong) doubles the
 // workgroup count for chunks too short to fill the 256 CUs with 32-row tiles.
-// Shape threshold in force (a debug hook sets it; see mc_kv.h).
+// Shape threshold and job packing in force (debug hooks set them).
 std::atomic<uint32_t> g_small_below{MC_PF_SMALL_BELOW};
+std::atomic<uint32_t> g_packing{1u};
+
+// Compute units of the current device (cached per device; 0 if unknown).
+uint32_t cu_count() {
+    static std::atomic<uint32_t> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0u;
+    uint32_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0u) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            return 0u;
+        v = static_cast<uint32_t>(n);
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
 
 template <bool SMALL>
 struct PfShape {
@@ -97,13 +115,12 @@ constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (confli
 // reading each operand right before its MFMAs).
 constexpr int kOperandAhead = 8;
 
+// One job = (query tile, kv head, key split), numbered heavy tile first.
 template <bool PAGE_STEP, bool SMALL>
-__global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
-    __attribute__((amdgpu_waves_per_eu(2))) prefill_attn_kernel(
-    const uint16_t* __restrict__ q_rows, uint32_t T,
-    const uint32_t* __restrict__ d_base_pos, uint32_t layer,
+__device__ __forceinline__ void prefill_job(
+    const uint16_t* __restrict__ q_rows, uint32_t T, uint32_t base_pos, uint32_t layer,
     const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
-    uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S) {
+    uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S, uint32_t job) {
     constexpr uint32_t kThreads = PfShape<SMALL>::kThreads;
     constexpr uint32_t kQRows = PfShape<SMALL>::kQRows;
     constexpr uint32_t kBufs = PfShape<SMALL>::kBufs;
@@ -114,11 +131,10 @@ __global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
     __shared__ __align__(16) uint16_t sV[kBufs][kStep * kVPitch];
 
     const uint32_t ntq = (T + kQRows - 1u) / kQRows;
-    const uint32_t s = blockIdx.x % S;
-    const uint32_t kvh = (blockIdx.x / S) % kHkv;
-    const uint32_t qt = ntq - 1u - blockIdx.x / (S * kHkv);  // heavy tiles first
+    const uint32_t s = job % S;
+    const uint32_t kvh = (job / S) % kHkv;
+    const uint32_t qt = ntq - 1u - job / (S * kHkv);  // heavy tiles first
     const uint32_t tb = qt * kQRows;
-    const uint32_t base_pos = *d_base_pos;
     const uint32_t key_end = base_pos + tb + min(kQRows - 1u, T - 1u - tb);  // last key
     const uint32_t last = key_end / kStep;
     const uint32_t qsp = (last + S) / S;  // ceil((last+1)/S)
@@ -446,6 +462,51 @@ __global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
     }
 }
 
+// grid = one workgroup per job. Jobs are dispatched to CUs as they free up,
+// heavy first, which packs well while the jobs are many or of very different
+// sizes. With S == 1, between two and three jobs per resident workgroup slot
+// (`slots`, 0 = off) and a prefix of at least T/4 (jobs of similar size),
+// that greedy order leaves a third round of jobs on a few CUs; there the
+// last `slots` workgroups run a fixed packing instead and the others exit at
+// once: t = n - 2*slots slots take three of the 3t lightest jobs each
+// (snake order), the others two of the remaining ones (heaviest with
+// lightest). Every job is computed the same way in both modes.
+template <bool PAGE_STEP, bool SMALL>
+__global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
+    __attribute__((amdgpu_waves_per_eu(2))) prefill_attn_kernel(
+    const uint16_t* __restrict__ q_rows, uint32_t T,
+    const uint32_t* __restrict__ d_base_pos, uint32_t layer,
+    const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
+    uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S, uint32_t slots) {
+    const uint32_t base_pos = *d_base_pos;
+    const uint32_t n = gridDim.x;
+    uint32_t jobs[3] = {blockIdx.x, 0u, 0u}, nj = 1u;
+    if constexpr (!SMALL) {
+        if (S == 1u && slots > 0u && n > 2u * slots && n <= 3u * slots &&
+            4ull * base_pos >= T) {
+            if (blockIdx.x < n - slots) return;
+            const uint32_t w = blockIdx.x - (n - slots);
+            const uint32_t t = n - 2u * slots, pairs = slots - t, b0 = 2u * pairs;
+            if (w < pairs) {
+                jobs[0] = w;
+                jobs[1] = b0 - 1u - w;
+                nj = 2u;
+            } else {
+                const uint32_t u = w - pairs;
+                jobs[0] = b0 + u;
+                jobs[1] = b0 + 2u * t - 1u - u;
+                jobs[2] = b0 + 2u * t + u;
+                nj = 3u;
+            }
+        }
+    }
+    for (uint32_t i = 0; i < nj; ++i) {
+        if (i > 0u) __syncthreads();  // LDS buffers are reused by the next job
+        prefill_job<PAGE_STEP, SMALL>(q_rows, T, base_pos, layer, pt, pool, ly, out, partials,
+                                      S, jobs[i]);
+    }
+}
+
 // grid = T*16 (block = (t, qh)), block = 128 (thread = dim).
 __global__ void __launch_bounds__(128) prefill_merge_kernel(
     const float* __restrict__ partials, uint32_t S, uint32_t T,
@@ -483,6 +544,12 @@ extern "C" mc_status_t mc_kv_debug_prefill_small_below(uint32_t workgroups,
     return MC_OK;
 }
 
+extern "C" mc_status_t mc_kv_debug_prefill_packing(uint32_t enable, uint32_t* previous) {
+    const uint32_t prev = mckv::g_packing.exchange(enable ? 1u : 0u);
+    if (previous != nullptr) *previous = prev;
+    return MC_OK;
+}
+
 extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_t tokens,
                                                const uint32_t* d_base_pos, uint32_t layer,
                                                const uint32_t* d_page_table,
@@ -512,7 +579,9 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
                        dim3(kHkv * ((tokens + PfShape<SM>::kQRows - 1u) / PfShape<SM>::kQRows) * \
                             S_kv),                                                           \
                        dim3(PfShape<SM>::kThreads), 0, st, d_q_rows, tokens, d_base_pos, layer, \
-                       d_page_table, d_kv_pool, ly, d_out, d_partials, S_kv)
+                       d_page_table, d_kv_pool, ly, d_out, d_partials, S_kv, slots)
+    // resident 32-row workgroup slots: one per CU (LDS-limited)
+    const uint32_t slots = small ? 0u : g_packing.load(std::memory_order_relaxed) ? cu_count() : 0u;
     const bool page_step = (1u << ly.log2p) >= kStep;
     if (page_step) {
         if (small) MC_PF_LAUNCH(true, true);

@@ -152,6 +152,15 @@ def debug_prefill_small_below(workgroups: int) -> int:
     return prev.value
 
 
+def debug_prefill_packing(enable: bool) -> bool:
+    """Turns the fixed prefill job packing on or off and returns the previous
+    setting. Debug hook, no reference counterpart."""
+    prev = C.c_uint32(0)
+    check(lib().mc_kv_debug_prefill_packing(1 if enable else 0, C.byref(prev)),
+          "debug_prefill_packing")
+    return bool(prev.value)
+
+
 def launch_decode_advance(d_seq, d_next_token, d_seq_len, stream=None) -> None:
     check(lib().mc_kv_decode_advance(_ptr(d_seq), _ptr(d_next_token), _ptr(d_seq_len),
                                      _stream(stream)), "launch_decode_advance")

@@ -16,7 +16,7 @@ POISON = 0xDCBA
 
 
 def run_prefill(kvm, orc, dev, T, base, S, P=32, seed=0, sentinel=False, check=True,
-                abs_check=True, kgrow=0.0):
+                abs_check=True, kgrow=0.0, inputs=False):
     import torch
     rng = np.random.default_rng(seed)
     ctx = base + T
@@ -52,6 +52,8 @@ def run_prefill(kvm, orc, dev, T, base, S, P=32, seed=0, sentinel=False, check=T
         else:  # the sentinel rows hold |V| = 40; check the unaffected rows
             st40 = orc.compare_bf16(got[:40], ref[:40])
             assert st40["max_abs"] < 2e-2 and st40["mean_abs"] < 2e-3, st40
+    if inputs:
+        return got, (q, pool, pt, maxp, layer)
     return got
 
 
@@ -123,3 +125,26 @@ def test_prefill_both_shapes(kvm, orc, dev, T, base, S, P, kgrow):
         kvm.debug_prefill_small_below(prev)
     if S == 1:
         assert np.array_equal(wide, narrow), "32-row and 16-row shapes differ"
+
+
+def test_prefill_packed_jobs(kvm, orc, dev):
+    """8448 rows after an 8448-token prefix: 528 jobs of similar size for 256
+    CUs, where one workgroup per CU runs a fixed two- or three-job packing
+    instead of greedy dispatch. Both schedules give bit-identical outputs;
+    row windows at the start, middle and end are checked against the oracle
+    (rows t0..t1 of a chunk are the chunk of those rows at base + t0)."""
+    T, base, P = 8448, 8448, 64
+    prev = kvm.debug_prefill_packing(True)
+    try:
+        packed, (q, pool, pt, maxp, layer) = run_prefill(kvm, orc, dev, T, base, 1, P=P,
+                                                         seed=3, check=False, inputs=True)
+        kvm.debug_prefill_packing(False)
+        greedy = run_prefill(kvm, orc, dev, T, base, 1, P=P, seed=3, check=False)
+    finally:
+        kvm.debug_prefill_packing(prev)
+    assert np.array_equal(packed, greedy), "packed and greedy schedules differ"
+    for t0 in (0, 4200, T - 8):
+        ref = orc.attn_ref(q[t0:t0 + 8], 8, base + t0, layer, pool, pt, P, maxp)
+        st = orc.compare_bf16(packed[t0:t0 + 8], ref)
+        assert st["rel_l2"] < 1e-2 and st["cos"] > 0.9999, (t0, st)
+        assert st["max_abs"] < 2e-2 and st["mean_abs"] < 2e-3, (t0, st)
