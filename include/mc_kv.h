@@ -224,13 +224,13 @@ mc_status_t mc_debug_session_info(mc_session_t session, uint32_t* seq_len,
 /* Copies the first n token ids of the device sequence (n <= seq_len). */
 mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n);
 
-/* Prefill workgroup shape: launches with fewer than `workgroups` 32-row
- * workgroups use 16-row ones (bit-identical results for S_kv = 1; with key
- * splits the split boundaries follow each tile's last row). Default 512;
- * 0 keeps 32-row tiles always, 0xFFFFFFFF selects 16-row tiles always. The
- * previous value is stored to *previous when that is not NULL. Process-wide;
- * for tests that run both shapes on the same inputs. */
-mc_status_t mc_kv_debug_prefill_small_below(uint32_t workgroups, uint32_t* previous);
+/* Prefill workgroup shape: 0 = 32 query rows on 8 waves, 1 = 16 rows on 4
+ * waves, 2 = 16 rows on two 4-wave halves taking alternate key steps,
+ * 0xFFFFFFFF = chosen per launch (default). All compute the same softmax;
+ * shapes differ in tile boundaries (key splits) and summation order, within
+ * the attention tolerance. The previous value is stored to *previous when
+ * that is not NULL. Process-wide; for tests that run every shape. */
+mc_status_t mc_kv_debug_prefill_shape(uint32_t shape, uint32_t* previous);
 
 /* Prefill job packing: with key splits off, two to three 32-row jobs per CU
  * and a prefix of at least T/4, one workgroup per CU runs a fixed 2-3 job

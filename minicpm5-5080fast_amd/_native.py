@@ -70,7 +70,7 @@ _SIGS = {
                                           _u32, _P]),
     "mc_kv_decode_advance": (C.c_int, [_P, _P, _P, _P]),
     "mc_kv_batch_advance": (C.c_int, [_P, _P, _P, _u32, _P]),
-    "mc_kv_debug_prefill_small_below": (C.c_int, [_u32, _P]),
+    "mc_kv_debug_prefill_shape": (C.c_int, [_u32, _P]),
     "mc_kv_debug_prefill_packing": (C.c_int, [_u32, _P]),
 }
 

@@ -17,8 +17,10 @@
 //
 // MI355X design: one 512-thread workgroup (8 wave64, 2 per SIMD) per (kv
 // head, 32-row q tile, key split); heavy (late) q tiles are launched first.
-// Launches with fewer than 512 such workgroups use 256-thread workgroups of
-// 16 rows instead (4 waves, two LDS buffers), so small T still fills the CUs.
+// Launches with fewer than 512 such workgroups use 16-row tiles instead: as
+// two 4-wave halves that take alternate key steps and merge their softmax
+// states in LDS (no key splits, at most two tiles per CU: the heaviest
+// causal tile sets the time), else as 256-thread workgroups two per CU.
 // The 32 rows x 8 query heads of a KV head are 256 query vectors: wave w owns
 // two 16-column groups, group g holding rows 4w + 2g + {0, 1} x heads 0..7.
 // Keys stream in 64-position steps gathered through the page table into LDS
@@ -52,14 +54,19 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Workgroup shapes (template parameter SH):
+//   kRows32: 512 threads, 8 waves, 32 q rows, three LDS buffers, ping-pong
+//            P.V; one workgroup per CU (107 KB LDS);
+//   kRows16: 256 threads, 4 waves, 16 q rows, two LDS buffers; two per CU;
+//   kHalves: 512 threads, 16 q rows, two 4-wave halves on alternate key steps
+//            (two LDS buffers each) merged in LDS at the end; one per CU.
+constexpr uint32_t kRows32 = 0u, kRows16 = 1u, kHalves16 = 2u;
 #ifndef MC_PF_SMALL_BELOW
-#define MC_PF_SMALL_BELOW 512u  // default: 32-row workgroups (2 per CU) below which 16-row tiles are used
+#define MC_PF_SMALL_BELOW 512u  // 32-row workgroups (2 per CU) below which 16-row shapes are used
 #endif
-// Workgroup shape: 512 threads (8 waves, 32 q rows) by default; SMALL = 256
-// threads (4 waves, 16 q rows, two LDS buffers, no ping-pong) doubles the
-// workgroup count for chunks too short to fill the 256 CUs with 32-row tiles.
-// Shape threshold and job packing in force (debug hooks set them).
-std::atomic<uint32_t> g_small_below{MC_PF_SMALL_BELOW};
+// Forced shape (debug hook; kAutoShape = chosen per launch) and job packing.
+constexpr uint32_t kAutoShape = 0xFFFFFFFFu;
+std::atomic<uint32_t> g_shape{kAutoShape};
 std::atomic<uint32_t> g_packing{1u};
 
 // Compute units of the current device (cached per device; 0 if unknown).
@@ -79,11 +86,12 @@ uint32_t cu_count() {
     return v;
 }
 
-template <bool SMALL>
+template <uint32_t SH>
 struct PfShape {
-    static constexpr uint32_t kThreads = SMALL ? 256u : 512u;
-    static constexpr uint32_t kQRows = kThreads / 16u;  // q rows per workgroup (4 per wave)
-    static constexpr uint32_t kBufs = SMALL ? 2u : 3u;  // LDS K/V buffers (see the ping-pong)
+    static constexpr uint32_t kThreads = SH == kRows16 ? 256u : 512u;
+    static constexpr uint32_t kHalves = SH == kHalves16 ? 2u : 1u;  // key-step sets
+    static constexpr uint32_t kQRows = kThreads / kHalves / 16u;  // q rows (4 per wave)
+    static constexpr uint32_t kBufs = SH == kRows32 ? 3u : 2u;  // LDS K/V buffers per half
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) {
@@ -116,19 +124,20 @@ constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (confli
 constexpr int kOperandAhead = 8;
 
 // One job = (query tile, kv head, key split), numbered heavy tile first.
-template <bool PAGE_STEP, bool SMALL>
+template <bool PAGE_STEP, uint32_t SH>
 __device__ __forceinline__ void prefill_job(
     const uint16_t* __restrict__ q_rows, uint32_t T, uint32_t base_pos, uint32_t layer,
     const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
     uint16_t* __restrict__ out, float* __restrict__ partials, uint32_t S, uint32_t job) {
-    constexpr uint32_t kThreads = PfShape<SMALL>::kThreads;
-    constexpr uint32_t kQRows = PfShape<SMALL>::kQRows;
-    constexpr uint32_t kBufs = PfShape<SMALL>::kBufs;
-    constexpr uint32_t kKeysPerPass = kThreads / 16u;  // keys one gather pass covers
+    constexpr uint32_t kThreads = PfShape<SH>::kThreads;
+    constexpr uint32_t kQRows = PfShape<SH>::kQRows;
+    constexpr uint32_t kBufs = PfShape<SH>::kBufs;
+    constexpr uint32_t kH = PfShape<SH>::kHalves;
+    constexpr uint32_t kKeysPerPass = kThreads / kH / 16u;  // keys one gather pass covers
     constexpr int kPass = 32 / (int)kKeysPerPass;      // passes per 32-key half
     constexpr int kStage = 2 * kNH * kPass;            // 16-byte chunks per thread and step
-    __shared__ __align__(16) uint16_t sK[kBufs][kStep * kKPitch];
-    __shared__ __align__(16) uint16_t sV[kBufs][kStep * kVPitch];
+    __shared__ __align__(16) uint16_t sK[kH * kBufs][kStep * kKPitch];
+    __shared__ __align__(16) uint16_t sV[kH * kBufs][kStep * kVPitch];
 
     const uint32_t ntq = (T + kQRows - 1u) / kQRows;
     const uint32_t s = job % S;
@@ -142,7 +151,12 @@ __device__ __forceinline__ void prefill_job(
     const uint32_t js1 = min(js0 + qsp - 1u, last);
 
     const uint32_t tid = threadIdx.x;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // kHalves16: waves w and w + 4 own the same query columns; half h takes
+    // the steps js0 + h, js0 + h + 2, ... into its own LDS buffers.
+    const uint32_t half = kH == 2u ? wave_id >> 2 : 0u;
+    const uint32_t wave = kH == 2u ? wave_id & 3u : wave_id;
+    const uint32_t hb = half * kBufs;  // this half's first LDS buffer
     const uint32_t lane = tid & 63u;
     const uint32_t col = lane & 15u;
     const uint32_t grp = lane >> 4;
@@ -182,8 +196,13 @@ __device__ __forceinline__ void prefill_job(
 
     // Cooperative gather: per 32-key half, thread tid moves the 16-byte K and
     // V chunks of key tid/16, dims 8*(tid%16) (16 threads per 256-byte row).
-    uint4 stage[kStage];  // [K chunks of each half and pass, then V chunks]
-    const uint32_t kkey = tid >> 4, kdb = tid & 15u;
+    // [K chunks of each half and pass, then V chunks]; zero until the first
+    // gather (a half without steps stores zeros)
+    uint4 stage[kStage];
+#pragma unroll
+    for (int r = 0; r < kStage; ++r) stage[r] = make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t gtid = tid & (kThreads / kH - 1u);  // gather thread within the half
+    const uint32_t kkey = gtid >> 4, kdb = gtid & 15u;
     // key (within the step) and K/V half of stage slot r
     auto key_of = [&](int r) {
         const int rem = r % (kNH * kPass);
@@ -250,8 +269,9 @@ __device__ __forceinline__ void prefill_job(
 #pragma unroll
         for (int r = 0; r < kNH * kPass; ++r) {
             const uint32_t key = key_of(r);
-            *reinterpret_cast<uint4*>(&sK[b][key * kKPitch + kdb * 8u]) = stage[r];
-            *reinterpret_cast<uint4*>(&sV[b][key * kVPitch + kdb * 8u]) = stage[kNH * kPass + r];
+            *reinterpret_cast<uint4*>(&sK[hb + b][key * kKPitch + kdb * 8u]) = stage[r];
+            *reinterpret_cast<uint4*>(&sV[hb + b][key * kVPitch + kdb * 8u]) =
+                stage[kNH * kPass + r];
         }
     };
 
@@ -263,17 +283,18 @@ __device__ __forceinline__ void prefill_job(
     constexpr float kMoveSlack = 8.f / kC;  // 8 in log2 units, in raw score units
     constexpr float kSumCap = 256.f;        // lane sum of p that still bounds p by 2^8
     uint32_t pgn[kStage] = {};
-    if (js0 <= js1) {
-        page_ids(js0, pgn);
-        gather(js0, pgn);
-        if (js0 < js1) page_ids(js0 + 1u, pgn);
+    const uint32_t jsf = js0 + half;  // this half's first step
+    if (jsf <= js1) {
+        page_ids(jsf, pgn);
+        gather(jsf, pgn);
+        if (jsf + kH <= js1) page_ids(jsf + kH, pgn);
     }
     // Ping-pong: waves 4..7 (the second wave on each SIMD) add step j's P.V
     // at the start of step j+1, so that on every SIMD one wave runs MFMA
     // while the other runs the softmax. Three LDS buffers keep step j's V
     // intact until then (a wave that writes step j+1's buffer has passed the
     // barrier of step j, so all waves have finished step j-1).
-    const bool late_pv = !SMALL && wave >= 4u;
+    const bool late_pv = SH == kRows32 && wave >= 4u;
     // P of the current step; late waves consume it at the start of the next
     // step, before that step's softmax overwrites it.
     bf16x8 pb[G][kNH];
@@ -311,16 +332,22 @@ __device__ __forceinline__ void prefill_job(
         }
     };
     int b = 0;
-    for (uint32_t js = js0; js <= js1; ++js, bprev = b, b = (b + 1 == (int)kBufs) ? 0 : b + 1) {
+    // iterations: the same count for both halves (barriers). A half whose
+    // step is past js1 in the last one (act false) stores its last staged
+    // data (or zeros) and masks every key, which leaves its state unchanged.
+    const uint32_t nit = js0 <= js1 ? (js1 - js0) / kH + 1u : 0u;
+    for (uint32_t it = 0; it < nit; ++it, bprev = b, b = (b + 1 == (int)kBufs) ? 0 : b + 1) {
+        const uint32_t js = js0 + it * kH + half;
+        const bool act = kH == 1u || js <= js1;  // wave-uniform
         put(b);
         __syncthreads();
-        if (js < js1) {
-            gather(js + 1u, pgn);
-            if (js + 1u < js1) page_ids(js + 2u, pgn);
+        if (js + kH <= js1) {
+            gather(js + kH, pgn);
+            if (js + 2u * kH <= js1) page_ids(js + 2u * kH, pgn);
         }
-        const uint16_t* K = sK[b];
-        const uint16_t* Vt = sV[b];
-        if (late_pv && js > js0) pv(sV[bprev], pb);
+        const uint16_t* K = sK[hb + b];
+        const uint16_t* Vt = sV[hb + b];
+        if (late_pv && js > js0) pv(sV[hb + bprev], pb);
         // S^T blocks: key block kb (keys 16kb + row), lane col = query column.
         f32x4 sacc[kNKB][G];
         {
@@ -346,7 +373,7 @@ __device__ __forceinline__ void prefill_job(
         }
         // Keys of this lane: 32*js + 16*kb + 4*grp + j. Only steps that reach
         // past the tile's first row can hold masked keys (wave-uniform test).
-        if (js * kStep + kStep - 1u > base_pos + tb) {
+        if (!act || js * kStep + kStep - 1u > base_pos + tb) {
             const uint32_t pos0 = js * kStep + 4u * grp;
 #pragma unroll
             for (int g = 0; g < G; ++g)
@@ -354,7 +381,7 @@ __device__ __forceinline__ void prefill_job(
                 for (int kb = 0; kb < kNKB; ++kb)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        if (pos0 + 16u * kb + (uint32_t)j > base_pos + row[g])
+                        if (!act || pos0 + 16u * kb + (uint32_t)j > base_pos + row[g])
                             sacc[kb][g][j] = -INFINITY;
         }
 #pragma unroll
@@ -421,7 +448,46 @@ __device__ __forceinline__ void prefill_job(
         }
         if (!late_pv) pv(Vt, pb);
     }
-    if (late_pv && js0 <= js1) pv(sV[bprev], pb);
+    if (late_pv && js0 <= js1) pv(sV[hb + bprev], pb);
+    if constexpr (kH == 2u) {
+        // Fold half 1's state into half 0 through LDS (the K buffers, free
+        // after the barrier): per column M = max(m0, m1), factors
+        // exp2((m_h - M) * c) (0 for a half that saw no key), l and acc scaled
+        // and summed. Per lane: G (m, l) pairs and G * 8 acc quads.
+        static_assert(sizeof(float2) * G * 64u * 4u + sizeof(f32x4) * G * 8u * 64u * 4u <=
+                          sizeof(sK),
+                      "state fits the K buffers");
+        f32x4* sa = reinterpret_cast<f32x4*>(&sK[0][0]) + wave * (G * 8u * 64u) + lane;
+        float2* sml = reinterpret_cast<float2*>(reinterpret_cast<f32x4*>(&sK[0][0]) +
+                                                4u * G * 8u * 64u) +
+                      wave * (G * 64u) + lane;
+        __syncthreads();
+        if (half == 1u) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                sml[g * 64] = make_float2(m_run[g], l_run[g]);
+#pragma unroll
+                for (int db = 0; db < 8; ++db) sa[(g * 8 + db) * 64] = acc[g][db];
+            }
+        }
+        __syncthreads();
+        if (half == 1u) return;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float2 ml = sml[g * 64];
+            const float M = fmaxf(m_run[g], ml.x);
+            const float f0 =
+                m_run[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[g] - M) * kC);
+            const float f1 = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ml.x - M) * kC);
+            m_run[g] = M;
+            l_run[g] = l_run[g] * f0 + ml.y * f1;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                acc[g][db] = acc[g][db] * f0 + sa[(g * 8 + db) * 64] * f1;
+                __builtin_amdgcn_sched_barrier(0);  // one quad in flight: no register peak
+            }
+        }
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         l_run[g] += __shfl_xor(l_run[g], 16);
@@ -471,8 +537,8 @@ __device__ __forceinline__ void prefill_job(
 // once: t = n - 2*slots slots take three of the 3t lightest jobs each
 // (snake order), the others two of the remaining ones (heaviest with
 // lightest). Every job is computed the same way in both modes.
-template <bool PAGE_STEP, bool SMALL>
-__global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
+template <bool PAGE_STEP, uint32_t SH>
+__global__ void __launch_bounds__(PfShape<SH>::kThreads)
     __attribute__((amdgpu_waves_per_eu(2))) prefill_attn_kernel(
     const uint16_t* __restrict__ q_rows, uint32_t T,
     const uint32_t* __restrict__ d_base_pos, uint32_t layer,
@@ -481,7 +547,7 @@ __global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
     const uint32_t base_pos = *d_base_pos;
     const uint32_t n = gridDim.x;
     uint32_t jobs[3] = {blockIdx.x, 0u, 0u}, nj = 1u;
-    if constexpr (!SMALL) {
+    if constexpr (SH == kRows32) {
         if (S == 1u && slots > 0u && n > 2u * slots && n <= 3u * slots &&
             4ull * base_pos >= T) {
             if (blockIdx.x < n - slots) return;
@@ -502,7 +568,7 @@ __global__ void __launch_bounds__(PfShape<SMALL>::kThreads)
     }
     for (uint32_t i = 0; i < nj; ++i) {
         if (i > 0u) __syncthreads();  // LDS buffers are reused by the next job
-        prefill_job<PAGE_STEP, SMALL>(q_rows, T, base_pos, layer, pt, pool, ly, out, partials,
+        prefill_job<PAGE_STEP, SH>(q_rows, T, base_pos, layer, pt, pool, ly, out, partials,
                                       S, jobs[i]);
     }
 }
@@ -537,9 +603,12 @@ __global__ void __launch_bounds__(128) prefill_merge_kernel(
 
 using namespace mckv;
 
-extern "C" mc_status_t mc_kv_debug_prefill_small_below(uint32_t workgroups,
-                                                       uint32_t* previous) {
-    const uint32_t prev = mckv::g_small_below.exchange(workgroups);
+extern "C" mc_status_t mc_kv_debug_prefill_shape(uint32_t shape, uint32_t* previous) {
+    if (shape > mckv::kHalves16 && shape != mckv::kAutoShape) {
+        set_error("mc_kv_debug_prefill_shape: shape %u is not 0, 1, 2 or 0xFFFFFFFF", shape);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    const uint32_t prev = mckv::g_shape.exchange(shape);
     if (previous != nullptr) *previous = prev;
     return MC_OK;
 }
@@ -568,12 +637,23 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
         return MC_E_INVALID_ARGUMENT;
     }
     hipStream_t st = (hipStream_t)stream;
-    // 16-row tiles when 32-row tiles would give fewer than two workgroups per
-    // CU (measured: T=2048 67 -> 60 us, T=4096 125 -> 118 us); both shapes
-    // compute every row the same way (with S_kv > 1 the split boundaries
-    // follow each tile's last row, so they differ between the shapes).
-    const uint32_t ntq32 = (tokens + PfShape<false>::kQRows - 1u) / PfShape<false>::kQRows;
-    const bool small = kHkv * ntq32 * S_kv < g_small_below.load(std::memory_order_relaxed);
+    // Shape: 32-row tiles while they give at least two workgroups per CU;
+    // below that 16-row tiles, as two halves on alternate key steps when the
+    // launch has no key splits and at most two 16-row jobs per CU (the
+    // heaviest causal tile then sets the time, and the halves take it at
+    // twice the rate), else as 4-wave workgroups two per CU. Measured
+    // (base 0): T=2048 67 -> 60 (16 rows) -> 47.5 us (halves), T=4096
+    // 125 -> 118 -> 99.7 us; T=6144 178.5 us with 4-wave workgroups against
+    // 210 with halves. With S_kv > 1 a tile's split boundaries follow its
+    // last row, so they differ between 32- and 16-row tiles.
+    const uint32_t ntq32 = (tokens + 31u) / 32u, ntq16 = (tokens + 15u) / 16u;
+    const uint32_t cus = cu_count();
+    uint32_t shape = g_shape.load(std::memory_order_relaxed);
+    if (shape == kAutoShape) {
+        if (kHkv * ntq32 * S_kv >= MC_PF_SMALL_BELOW) shape = kRows32;
+        else if (S_kv == 1u && kHkv * ntq16 <= 2u * (cus ? cus : 256u)) shape = kHalves16;
+        else shape = kRows16;
+    }
 #define MC_PF_LAUNCH(PG, SM)                                                                 \
     hipLaunchKernelGGL((prefill_attn_kernel<PG, SM>),                                        \
                        dim3(kHkv * ((tokens + PfShape<SM>::kQRows - 1u) / PfShape<SM>::kQRows) * \
@@ -581,14 +661,22 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
                        dim3(PfShape<SM>::kThreads), 0, st, d_q_rows, tokens, d_base_pos, layer, \
                        d_page_table, d_kv_pool, ly, d_out, d_partials, S_kv, slots)
     // resident 32-row workgroup slots: one per CU (LDS-limited)
-    const uint32_t slots = small ? 0u : g_packing.load(std::memory_order_relaxed) ? cu_count() : 0u;
+    const uint32_t slots =
+        shape == kRows32 && g_packing.load(std::memory_order_relaxed) ? cus : 0u;
     const bool page_step = (1u << ly.log2p) >= kStep;
-    if (page_step) {
-        if (small) MC_PF_LAUNCH(true, true);
-        else MC_PF_LAUNCH(true, false);
-    } else {
-        if (small) MC_PF_LAUNCH(false, true);
-        else MC_PF_LAUNCH(false, false);
+    switch (shape) {
+        case kRows32:
+            if (page_step) MC_PF_LAUNCH(true, kRows32);
+            else MC_PF_LAUNCH(false, kRows32);
+            break;
+        case kRows16:
+            if (page_step) MC_PF_LAUNCH(true, kRows16);
+            else MC_PF_LAUNCH(false, kRows16);
+            break;
+        default:
+            if (page_step) MC_PF_LAUNCH(true, kHalves16);
+            else MC_PF_LAUNCH(false, kHalves16);
+            break;
     }
 #undef MC_PF_LAUNCH
     if (S_kv > 1u)

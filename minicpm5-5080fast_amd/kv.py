@@ -142,13 +142,15 @@ def launch_attn_prefill_flash(d_q_rows, tokens, d_base_pos, layer, d_page_table,
                                         _stream(stream)), "launch_attn_prefill_flash")
 
 
-def debug_prefill_small_below(workgroups: int) -> int:
-    """Sets the prefill shape threshold (32-row workgroup count below which
-    16-row workgroups are used; 0 = never, 0xFFFFFFFF = always) and returns
-    the previous one. Debug hook, no reference counterpart."""
+PREFILL_SHAPE_AUTO = 0xFFFFFFFF
+
+
+def debug_prefill_shape(shape: int) -> int:
+    """Forces the prefill workgroup shape (0 = 32 rows, 1 = 16 rows on 4
+    waves, 2 = 16 rows on two halves, PREFILL_SHAPE_AUTO = per launch) and
+    returns the previous setting. Debug hook, no reference counterpart."""
     prev = C.c_uint32(0)
-    check(lib().mc_kv_debug_prefill_small_below(workgroups, C.byref(prev)),
-          "debug_prefill_small_below")
+    check(lib().mc_kv_debug_prefill_shape(shape, C.byref(prev)), "debug_prefill_shape")
     return prev.value
 
 

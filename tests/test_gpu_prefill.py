@@ -108,23 +108,26 @@ def test_prefill_growing_scores(kvm, orc, dev, T, base, S):
                                               (300, 40, 4, 64, 9.0), (150, 29, 1, 8, 0.0),
                                               (96, 8448, 1, 64, 0.0), (1, 0, 1, 32, 0.0),
                                               (512, 0, 1, 64, 9.0)])
-def test_prefill_both_shapes(kvm, orc, dev, T, base, S, P, kgrow):
-    """The 32-row workgroups (8 waves, ping-pong P.V) and the 16-row ones
-    (4 waves) compute every row the same way: without key splits the outputs
-    are bit-identical. With S > 1 a tile's split boundaries follow its last
-    row, so the partials group differently and both shapes are held to the
-    oracle tolerance instead. The launch picks the shape from the workgroup
-    count; the debug hook forces each one here."""
-    prev = kvm.debug_prefill_small_below(0)
+def test_prefill_all_shapes(kvm, orc, dev, T, base, S, P, kgrow):
+    """The three workgroup shapes: 32 query rows on 8 waves (ping-pong P.V),
+    16 rows on 4 waves, and 16 rows on two 4-wave halves that take alternate
+    key steps and merge their softmax states in LDS. The launch picks one per
+    call; the debug hook forces each here. Every shape is held to the oracle
+    tolerance, and without key splits the two 1-set shapes (same steps, same
+    order) are bit-identical."""
+    outs = {}
+    prev = kvm.debug_prefill_shape(0)
     try:
-        wide = run_prefill(kvm, orc, dev, T, base, S, P=P, seed=T + S, kgrow=kgrow)
-        kvm.debug_prefill_small_below(0xFFFFFFFF)
-        narrow = run_prefill(kvm, orc, dev, T, base, S, P=P, seed=T + S, kgrow=kgrow,
-                             check=S > 1)
+        for shape in (0, 1, 2):
+            kvm.debug_prefill_shape(shape)
+            outs[shape] = run_prefill(kvm, orc, dev, T, base, S, P=P, seed=T + S, kgrow=kgrow)
     finally:
-        kvm.debug_prefill_small_below(prev)
+        kvm.debug_prefill_shape(prev)
     if S == 1:
-        assert np.array_equal(wide, narrow), "32-row and 16-row shapes differ"
+        assert np.array_equal(outs[0], outs[1]), "32-row and 16-row shapes differ"
+    for shape in (1, 2):
+        d = np.abs(orc.bf16_to_f32(outs[0]) - orc.bf16_to_f32(outs[shape]))
+        assert d.max() < 2e-2 and d.mean() < 2e-3, (shape, d.max(), d.mean())
 
 
 def test_prefill_packed_jobs(kvm, orc, dev):
