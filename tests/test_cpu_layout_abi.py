@@ -86,3 +86,24 @@ def test_error_convention(pkg, kvm):
     with pytest.raises(pkg.McError):
         kvm.launch_rope_kv(None, 1, None, 0, None, None, kvm.KvLayout(8, 32, 1), 5e6,
                            stream=0)
+
+
+def test_prefill_debug_hooks(pkg, kvm):
+    """The prefill shape and packing hooks (host state only, no GPU): a set
+    returns the previous value, and an unknown shape is rejected."""
+    prev = kvm.debug_prefill_shape(1)
+    try:
+        assert kvm.debug_prefill_shape(2) == 1
+        with pytest.raises(pkg.McError) as e:
+            kvm.debug_prefill_shape(3)
+        assert e.value.status == 1 and "shape" in str(e.value)
+        assert kvm.debug_prefill_shape(kvm.PREFILL_SHAPE_AUTO) == 2
+    finally:
+        kvm.debug_prefill_shape(prev)
+    assert prev == kvm.PREFILL_SHAPE_AUTO
+    was = kvm.debug_prefill_packing(False)
+    try:
+        assert kvm.debug_prefill_packing(True) is False
+    finally:
+        kvm.debug_prefill_packing(was)
+    assert was is True
