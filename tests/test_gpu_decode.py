@@ -446,3 +446,26 @@ def test_repeat_launch_and_graph_replay(kvm, orc, dev, ctx, C):
         run(e)
         torch.cuda.synchronize()
         assert np.array_equal(got, from_dev(e)), f"replay {k}"
+
+
+def _random_batch_cases(n, seed):
+    import random
+    rnd = random.Random(seed)
+    out = []
+    for i in range(n):
+        B = rnd.choice([1, 2, 3, 5, 8, 13, 20])
+        C = rnd.choice([64, 128, 256, 512, 48, 80])
+        ctx = rnd.choice([40, 300, 1000, 2500, 6000, 12000])
+        ph0 = rnd.random() < 0.5
+        step = max(0, min(rnd.choice([0, 1, 9, 37, 200]), (ctx - 2) // B))
+        out.append((B, C, ctx, ph0, step, 2000 + i))
+    return out
+
+
+@pytest.mark.parametrize("B,C,ctx,ph0,step,seed", _random_batch_cases(12, 7))
+def test_batch_random_cases(kvm, orc, dev, B, C, ctx, ph0, step, seed):
+    """Seeded random batched cases (slot count, chunk tier incl. non-multiples
+    of 64, context, phase0, ragged limits): bit-identical to single-session
+    calls and within tolerance of the oracle."""
+    print(f"B={B} C={C} ctx={ctx} ph0={ph0} step={step} seed={seed}", flush=True)
+    _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed=seed, step=step)

@@ -151,3 +151,27 @@ def test_prefill_packed_jobs(kvm, orc, dev):
         st = orc.compare_bf16(packed[t0:t0 + 8], ref)
         assert st["rel_l2"] < 1e-2 and st["cos"] > 0.9999, (t0, st)
         assert st["max_abs"] < 2e-2 and st["mean_abs"] < 2e-3, (t0, st)
+
+
+def _random_prefill_cases(n, seed):
+    import random
+    rnd = random.Random(seed)
+    out = []
+    for i in range(n):
+        T = rnd.choice([1, 2, 15, 33, 64, 100, 255, 300, 513, 700])
+        base = rnd.choice([0, 0, 1, 37, 64, 500, 2047, 3000])
+        S = 1 if T >= 2048 else min(8, 4096 // T)  # prefill_flash_split_kv
+        if rnd.random() < 0.4:
+            S = 1  # the session may pass S = 1 at any T
+        P = rnd.choice([8, 16, 32, 64])
+        kgrow = rnd.choice([0.0, 0.0, 4.0])
+        out.append((T, base, S, P, kgrow, 3000 + i))
+    return out
+
+
+@pytest.mark.parametrize("T,base,S,P,kgrow,seed", _random_prefill_cases(12, 11))
+def test_prefill_random_cases(kvm, orc, dev, T, base, S, P, kgrow, seed):
+    """Seeded random chunks (row count, prefix, key splits, page size, growing
+    key magnitude) under the automatic shape choice, against the oracle."""
+    print(f"T={T} base={base} S={S} P={P} kgrow={kgrow} seed={seed}", flush=True)
+    run_prefill(kvm, orc, dev, T, base, S, P=P, seed=seed, kgrow=kgrow)
