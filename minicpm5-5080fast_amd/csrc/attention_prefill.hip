@@ -16,7 +16,9 @@
 //     kernel (block per (t, qh)) folds the S_kv partials in ascending order.
 //
 // MI355X design: one 512-thread workgroup (8 wave64, 2 per SIMD) per (kv
-// head, 32-row q tile, key split); heavy (late) q tiles are launched first.
+// head, 32-row q tile, key split); heavy (late) q tiles are launched first,
+// and where greedy dispatch would leave a third round of similar-size jobs on
+// a few CUs, one workgroup per CU runs a fixed two/three-job packing.
 // Launches with fewer than 512 such workgroups use 16-row tiles instead: as
 // two 4-wave halves that take alternate key steps and merge their softmax
 // states in LDS (no key splits, at most two tiles per CU: the heaviest
