@@ -22,7 +22,8 @@
 // Launches with fewer than 512 such workgroups use 16-row tiles instead: as
 // two 4-wave halves that take alternate key steps and merge their softmax
 // states in LDS (no key splits, at most two tiles per CU: the heaviest
-// causal tile sets the time), else as 256-thread workgroups two per CU.
+// causal tile sets the time; each half waits only for its own waves, so the
+// halves run out of phase), else as 256-thread workgroups two per CU.
 // The 32 rows x 8 query heads of a KV head are 256 query vectors: wave w owns
 // two 16-column groups, group g holding rows 4w + 2g + {0, 1} x heads 0..7.
 // Keys stream in 64-position steps gathered through the page table into LDS
@@ -111,6 +112,9 @@ __device__ __forceinline__ float max_across_groups(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+#ifndef PF_HALF_BAR
+#define PF_HALF_BAR 1
+#endif
 #ifndef PF_STEP
 #define PF_STEP 64
 #endif
@@ -338,11 +342,34 @@ __device__ __forceinline__ void prefill_job(
     // step is past js1 in the last one (act false) stores its last staged
     // data (or zeros) and masks every key, which leaves its state unchanged.
     const uint32_t nit = js0 <= js1 ? (js1 - js0) / kH + 1u : 0u;
+    // kHalves16: each half reads and writes only its own LDS buffers, so per
+    // iteration it waits only for its own 4 waves (a counter in LDS), and the
+    // halves drift apart like two workgroups (one runs MFMA while the other
+    // runs the softmax). The wait is bounded: it cannot hang the kernel.
+    constexpr bool kHalfBar = kH == 2u && PF_HALF_BAR;
+    __shared__ uint32_t s_bar[2];
+    if constexpr (kHalfBar) {
+        if (tid < 2u) s_bar[tid] = 0u;
+        __syncthreads();
+    }
+    auto half_barrier = [&](uint32_t target) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0u) __hip_atomic_fetch_add(&s_bar[half], 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        for (uint32_t spin = 0; spin < (1u << 22); ++spin) {
+            const uint32_t v = __builtin_amdgcn_readfirstlane(__hip_atomic_load(
+                &s_bar[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            if (v >= target) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    };
     for (uint32_t it = 0; it < nit; ++it, bprev = b, b = (b + 1 == (int)kBufs) ? 0 : b + 1) {
         const uint32_t js = js0 + it * kH + half;
         const bool act = kH == 1u || js <= js1;  // wave-uniform
         put(b);
-        __syncthreads();
+        if constexpr (kHalfBar) half_barrier(4u * (it + 1u));
+        else __syncthreads();
         if (js + kH <= js1) {
             gather(js + kH, pgn);
             if (js + 2u * kH <= js1) page_ids(js + 2u * kH, pgn);
