@@ -115,13 +115,9 @@ __device__ __forceinline__ float max_across_groups(float x) {
 #ifndef PF_HALF_BAR
 #define PF_HALF_BAR 1
 #endif
-#ifndef PF_STEP
-#define PF_STEP 64
-#endif
-constexpr uint32_t kStep = PF_STEP;  // keys per step (32 or 64)
-constexpr int kNKB = kStep / 16;     // 16-key blocks per step
-constexpr int kNH = kStep / 32;      // 32-key halves per step (one PV MFMA each)
-static_assert(kStep == 32 || kStep == 64, "step of 32 or 64 keys");
+constexpr uint32_t kStep = 64;   // keys per step (32-key steps measured slower)
+constexpr int kNKB = kStep / 16;  // 16-key blocks per step
+constexpr int kNH = kStep / 32;   // 32-key halves per step (one PV MFMA each)
 constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
 constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (conflict-free tr reads)
 // LDS operand reads issued this many MFMA blocks ahead of their use (software
