@@ -169,9 +169,16 @@ def _random_prefill_cases(n, seed):
     return out
 
 
+@pytest.mark.parametrize("shape", ["auto", 2])
 @pytest.mark.parametrize("T,base,S,P,kgrow,seed", _random_prefill_cases(12, 11))
-def test_prefill_random_cases(kvm, orc, dev, T, base, S, P, kgrow, seed):
+def test_prefill_random_cases(kvm, orc, dev, T, base, S, P, kgrow, seed, shape):
     """Seeded random chunks (row count, prefix, key splits, page size, growing
-    key magnitude) under the automatic shape choice, against the oracle."""
-    print(f"T={T} base={base} S={S} P={P} kgrow={kgrow} seed={seed}", flush=True)
-    run_prefill(kvm, orc, dev, T, base, S, P=P, seed=seed, kgrow=kgrow)
+    key magnitude) against the oracle, under the automatic shape choice and
+    with the two-half shape forced (its per-half step barriers)."""
+    print(f"T={T} base={base} S={S} P={P} kgrow={kgrow} seed={seed} shape={shape}",
+          flush=True)
+    prev = kvm.debug_prefill_shape(kvm.PREFILL_SHAPE_AUTO if shape == "auto" else shape)
+    try:
+        run_prefill(kvm, orc, dev, T, base, S, P=P, seed=seed, kgrow=kgrow)
+    finally:
+        kvm.debug_prefill_shape(prev)
