@@ -132,14 +132,20 @@ mc_status_t mc_kv_rope_append(uint16_t* d_qkv, uint32_t tokens,
 /* ---- decode attention (split-KV flash decoding) ---- */
 
 /* launch_attention_decode (kernels.h:369-388, attention_decode.cu:1840-1964).
- * Attends positions 0..limit (limit = *d_pos) of one session. Chunk kernel
- * writes partials [16][max_chunks][130]; if limit < chunk_pos it writes
- * d_out [2048] directly. d_partials2 != NULL selects the two-level merge
- * (level-2 partials [16][32][130]); NULL selects the one-level merge. With
- * max_chunks <= 32 the two levels reduce exactly to one fold kernel.
+ * Attends positions 0..limit (limit = *d_pos) of one session and writes
+ * d_out [2048] bf16. d_partials [16][max_chunks][130] fp32 is scratch: the
+ * chunk kernel folds each workgroup's range of ceil(max_chunks / 256) chunks
+ * (one chunk when max_chunks <= 256, or when chunk_pos is not a multiple of
+ * 64) into one record {m, l, acc[128]} per query head, and a merge kernel
+ * folds the records (fixed order). Beyond 256 records per head (chunk_pos
+ * not a multiple of 64 and more than 256 chunks) the reference's merges run
+ * instead: two-level through d_partials2 ([16][32][130]) when it is not NULL
+ * and there are more than 32 records, else one-level. If limit < the range
+ * size the single workgroup writes d_out directly.
  * d_inv_freq != NULL enables phase0: q and k of position `limit` are rotated
  * from d_q_rows, K/V of `limit` are written to the pool (pool may be written
- * only in that case). chunk_pos must be a multiple of 16. */
+ * only in that case). chunk_pos must be a multiple of 16. d_page_table is
+ * read at entries 0..limit/P. */
 mc_status_t mc_kv_attention_decode(const uint16_t* d_q_rows, const uint32_t* d_pos,
                                    uint32_t layer, const uint32_t* d_page_table,
                                    uint16_t* d_kv_pool, mc_kv_layout_t layout,
@@ -157,7 +163,9 @@ mc_status_t mc_kv_attention_decode_merge(const float* d_partials,
                                          void* stream);
 
 /* Chunk kernel only (no merge): the test/bench twin of launch_attn_kv_h_test
- * (kernels.h:441-450) without the score scratch. */
+ * (kernels.h:441-450) without the score scratch. Writes the per-chunk
+ * partials [16][max_chunks][130] of chunks 0..limit/chunk_pos (one record
+ * per chunk), or d_out directly when limit < chunk_pos. */
 mc_status_t mc_kv_attention_decode_chunks(const uint16_t* d_q_rows,
                                           const uint32_t* d_pos, uint32_t layer,
                                           const uint32_t* d_page_table,
@@ -171,9 +179,10 @@ mc_status_t mc_kv_attention_decode_chunks(const uint16_t* d_q_rows,
 /* launch_attention_decode_batch (kernels.h:465-480,
  * attention_decode.cu:2120-2170). Slot s uses q row d_q_rows + s*2560,
  * limit *d_slot_pos[s], page table d_slot_pt[s], pool d_slot_kv[s]; writes
- * d_partials + s*16*max_chunks*130, d_partials2 + s*16*32*130 and
- * d_out + s*2048. Results are bit-identical to B single-session calls. The
- * three pointer tables live in device memory. */
+ * d_out + s*2048 and uses d_partials (B*16*max_chunks*130 floats) and
+ * d_partials2 (B*16*32*130) as scratch, as mc_kv_attention_decode does per
+ * slot. Outputs are bit-identical to B single-session calls. The three
+ * pointer tables live in device memory. B <= 64. */
 mc_status_t mc_kv_attention_decode_batch(const uint16_t* d_q_rows,
                                          const uint32_t* const* d_slot_pos,
                                          uint32_t B, uint32_t layer,
@@ -238,6 +247,24 @@ mc_status_t mc_kv_debug_prefill_shape(uint32_t shape, uint32_t* previous);
  * off (default on). The previous setting is stored to *previous when that is
  * not NULL. Process-wide; for tests that compare both schedules. */
 mc_status_t mc_kv_debug_prefill_packing(uint32_t enable, uint32_t* previous);
+
+/* Prefill status of the current device: *barrier_timeouts receives the
+ * number of per-half waits of the two-half prefill shape that ran out of
+ * their bound (about 0.1 s of polling) since the last reset; each such wait
+ * may have left wrong values in that launch's output, so any non-zero value
+ * is an error. reset != 0 clears the counter after reading. Synchronous:
+ * waits for work queued on the device's blocking streams. No reference
+ * counterpart (the reference's prefill uses workgroup barriers only). */
+mc_status_t mc_kv_debug_prefill_status(uint32_t* barrier_timeouts, uint32_t reset);
+
+/* Decode P.V precision (process-wide): 0 = P rounded to bf16 before P.V
+ * (default, the reference's HMMA path), 1 = fp32 P (the reference's
+ * MC_ATTN_HMMA_OFF fallback, attention_decode.cu:506-878), 0xFFFFFFFF = from
+ * the environment (MC_ATTN_HMMA_OFF set -> fp32 P, read once, as
+ * kernels.h:355-367 does). The previous value goes to *previous when not
+ * NULL. Switch between launches only: a captured graph keeps the kernels it
+ * was captured with. */
+mc_status_t mc_kv_debug_decode_fp32p(uint32_t fp32_p, uint32_t* previous);
 
 /* Library build identity, e.g. "minicpm-kv gfx950". */
 const char* mc_kv_build_info(void);

@@ -64,9 +64,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 //   kHalves: 512 threads, 16 q rows, two 4-wave halves on alternate key steps
 //            (two LDS buffers each) merged in LDS at the end; one per CU.
 constexpr uint32_t kRows32 = 0u, kRows16 = 1u, kHalves16 = 2u;
-#ifndef MC_PF_SMALL_BELOW
-#define MC_PF_SMALL_BELOW 512u  // 32-row workgroups (2 per CU) below which 16-row shapes are used
-#endif
+// 32-row workgroup count (2 per CU) below which the 16-row shapes are used.
+constexpr uint32_t kSmallBelow = 512u;
+// Polls of a per-half barrier before it gives up (s_sleep 1 = 64 clocks each,
+// about 2^22 * 64 / 2.4 GHz = 0.1 s): far beyond any legal wait, so it only
+// ends a wait that can never complete. A timed-out wait is counted in
+// g_barrier_timeouts (read by mc_kv_debug_prefill_status).
+constexpr uint32_t kHalfBarrierSpins = 1u << 22;
+__device__ uint32_t g_barrier_timeouts;
 // Forced shape (debug hook; kAutoShape = chosen per launch) and job packing.
 constexpr uint32_t kAutoShape = 0xFFFFFFFFu;
 std::atomic<uint32_t> g_shape{kAutoShape};
@@ -112,9 +117,6 @@ __device__ __forceinline__ float max_across_groups(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-#ifndef PF_HALF_BAR
-#define PF_HALF_BAR 1
-#endif
 constexpr uint32_t kStep = 64;   // keys per step (32-key steps measured slower)
 constexpr int kNKB = kStep / 16;  // 16-key blocks per step
 constexpr int kNH = kStep / 32;   // 32-key halves per step (one PV MFMA each)
@@ -341,8 +343,11 @@ __device__ __forceinline__ void prefill_job(
     // kHalves16: each half reads and writes only its own LDS buffers, so per
     // iteration it waits only for its own 4 waves (a counter in LDS), and the
     // halves drift apart like two workgroups (one runs MFMA while the other
-    // runs the softmax). The wait is bounded: it cannot hang the kernel.
-    constexpr bool kHalfBar = kH == 2u && PF_HALF_BAR;
+    // runs the softmax). The wait is bounded so that it cannot hang the
+    // kernel; a wait that runs out (the half would then race on LDS buffers
+    // still in use, so its output is unreliable) increments the device word
+    // g_barrier_timeouts with a vector atomic, which the host reads back.
+    constexpr bool kHalfBar = kH == 2u;
     __shared__ uint32_t s_bar[2];
     if constexpr (kHalfBar) {
         if (tid < 2u) s_bar[tid] = 0u;
@@ -352,12 +357,19 @@ __device__ __forceinline__ void prefill_job(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0u) __hip_atomic_fetch_add(&s_bar[half], 1u, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_WORKGROUP);
-        for (uint32_t spin = 0; spin < (1u << 22); ++spin) {
+        bool done = false;
+        for (uint32_t spin = 0; spin < kHalfBarrierSpins; ++spin) {
             const uint32_t v = __builtin_amdgcn_readfirstlane(__hip_atomic_load(
                 &s_bar[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-            if (v >= target) break;
+            if (v >= target) {
+                done = true;
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
         }
+        if (!done && lane == 0u)
+            __hip_atomic_fetch_add(&g_barrier_timeouts, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
     for (uint32_t it = 0; it < nit; ++it, bprev = b, b = (b + 1 == (int)kBufs) ? 0 : b + 1) {
@@ -644,6 +656,27 @@ extern "C" mc_status_t mc_kv_debug_prefill_packing(uint32_t enable, uint32_t* pr
     return MC_OK;
 }
 
+extern "C" mc_status_t mc_kv_debug_prefill_status(uint32_t* barrier_timeouts, uint32_t reset) {
+    if (barrier_timeouts == nullptr) {
+        set_error("mc_kv_debug_prefill_status: barrier_timeouts is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    // Synchronous on the null stream: waits for prefill launches in flight on
+    // blocking streams of the current device.
+    hipError_t e = hipMemcpyFromSymbol(barrier_timeouts, HIP_SYMBOL(mckv::g_barrier_timeouts),
+                                       sizeof(uint32_t), 0, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && reset) {
+        const uint32_t zero = 0u;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(mckv::g_barrier_timeouts), &zero, sizeof(zero), 0,
+                              hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        set_error("mc_kv_debug_prefill_status: %s", hipGetErrorString(e));
+        return MC_E_CUDA;
+    }
+    return MC_OK;
+}
+
 extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_t tokens,
                                                const uint32_t* d_base_pos, uint32_t layer,
                                                const uint32_t* d_page_table,
@@ -675,7 +708,7 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
     const uint32_t cus = cu_count();
     uint32_t shape = g_shape.load(std::memory_order_relaxed);
     if (shape == kAutoShape) {
-        if (kHkv * ntq32 * S_kv >= MC_PF_SMALL_BELOW) shape = kRows32;
+        if (kHkv * ntq32 * S_kv >= kSmallBelow) shape = kRows32;
         else if (S_kv == 1u && kHkv * ntq16 <= 2u * (cus ? cus : 256u)) shape = kHalves16;
         else shape = kRows16;
     }

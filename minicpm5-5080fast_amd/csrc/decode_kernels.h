@@ -1,0 +1,911 @@
+// decode_kernels.h - device code of the paged split-KV flash decoding for one
+// new token per session (single session and batched), shared by the two
+// translation units that instantiate it (bf16-P and fp32-P).
+//
+// Contract of the reference path (native/kernels/sm120/attention_decode.cu:
+// 966-1368 chunk kernel, 506-878 fp32-P SIMT variant, 1494-1595 merge_a /
+// merge_b, 1389-1407/1602-1626 batched twins, 1840-1964/2120-2170 launchers):
+//   * limit = *d_pos is the query position; keys/values 0..limit are attended.
+//   * Work is split in chunks of chunk_pos positions; chunk c covers
+//     [c*C, min(c*C+C-1, limit)]; chunks starting after limit do nothing.
+//   * Scores are fp32 dot(q, k) * (1/sqrt(128) as fp32); softmax runs online in
+//     16-position batches: mn = max(m, batch max), renew = exp(m - mn) (0 when
+//     m = -inf), p = exp(score - mn) in fp32 feeds l, and p rounded to bf16
+//     (RNE) feeds the P.V product (fp32-P mode: p itself feeds P.V, the
+//     reference's MC_ATTN_HMMA_OFF fallback).
+//   * A partial record is {m, l, acc[128]}; the merge folds records with
+//     M = max m over l != 0, f = exp(m - M), L = sum l f, A = sum acc f and
+//     writes bf16(A / L). A single record is written as the output directly.
+//   * Phase0 (inv_freq != NULL): the block owning position `limit` rotates that
+//     token's k from the qkv row, writes K and V of `limit` to the pool and uses
+//     the fresh values; q is rotated on the fly (LDS) and never written back.
+//
+// MI355X design (one 256-thread workgroup = 4 wave64 per (slot, kv head,
+// range of chunks); single-session 256/512-position tiers with at least 256
+// workgroups put both KV heads in one 512-thread workgroup, and batched
+// launches number their workgroups densely over the slots' existing chunk
+// groups). Each wave walks 16-position tiles t = wave, wave+4, ...
+// of each chunk and keeps one online-softmax state for all 8 query heads
+// of the KV head over the whole range; the 4 wave states are folded through
+// LDS once, into one record per query head; a second launch (merge_task)
+// folds the records. The next tile's loads are in flight while the current
+// tile computes.
+//   * Loads: K in operand layout - a lane (token = lane%16, group = lane/16)
+//     reads K dims [32m + 8*group, +8), m < 4, i.e. each instruction reads 64
+//     contiguous bytes of 16 rows. V as whole 256-byte head rows (16 lanes per
+//     row) into a wave-private, XOR-swizzled LDS tile. For the 64-position
+//     chunk tier K is row-loaded the same way and read back from LDS in the
+//     operand layout.
+//   * QK: S^T[16 pos][16 heads] = K (A operand) x Q^T (B operand, preloaded;
+//     heads 8..15 are zero padding) with four v_mfma_f32_16x16x32_bf16.
+//   * The D layout gives each lane 4 positions of one head; the batch max/sum
+//     combine the 4 lane groups with two row-swap permutes (16, 32).
+//   * P.V: O^T += V^T x P^T (v_mfma_f32_16x16x16bf16_1k; fp32-P: four
+//     v_mfma_f32_16x16x4f32). The V^T A operand comes from the LDS tile
+//     through the transposing read ds_read_b64_tr_b16; P^T (B operand) is the
+//     softmax output already in the right lanes. (The generic schedule for
+//     chunk sizes that are not a multiple of 64 keeps V in operand layout and
+//     transposes each 16x16 block exactly by an MFMA with an identity B
+//     operand.) acc ends up as 32 fp32 per lane: head lane%16, dims
+//     [32m + 8*group, +8).
+// Arithmetic intensity is ~8 flop/byte, so the kernel is HBM-bound; MFMA keeps
+// the VALU free for addressing and softmax.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "error.h"
+#include "kv_common.h"
+
+namespace mckv {
+namespace {
+// Cross-lane reductions without an LDS round trip. gfx950's row-swap
+// permutes applied to (x, x): permlane16_swap gives the 16-lane rows
+// (r0, r0, r2, r2) and (r1, r1, r3, r3), permlane32_swap the halves (lo, lo)
+// and (hi, hi). Combining the two results reduces lanes l, l^16 (then l^32)
+// with the same operands, in the same order, as xor shuffles would.
+__device__ __forceinline__ float swap16_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float swap32_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float swap16_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float swap32_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+// Max over all 64 lanes: DPP within quads, 8- and 16-lane mirrors, then the
+// row swaps (max is exact in any order).
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF,
+                                                         false)));  // quad_perm 1,0,3,2
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF,
+                                                         false)));  // quad_perm 2,3,0,1
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF,
+                                                         false)));  // row_half_mirror
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF,
+                                                         false)));  // row_mirror
+    return swap32_max(swap16_max(x));
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kThreads = 256;
+constexpr uint32_t kWaves = 4;
+constexpr uint32_t kTile = 16;
+constexpr uint32_t kPageCache = 128;  // page ids staged in LDS per block
+// Smallest single-session grid that takes two-head (512-thread) workgroups.
+constexpr uint32_t kKv2MinBlocks = 256;
+// Register tiles in each wave's load ring (one load group ahead).
+constexpr uint32_t kRing = 2;
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+struct Tile {
+    uint4 k[4];
+    uint4 v[4];
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) {
+    return __builtin_bit_cast(bf16x8, u);
+}
+__device__ __forceinline__ s16x4 half_s16x4(const uint4& u, int h) {
+    const uint2 x = h ? make_uint2(u.z, u.w) : make_uint2(u.x, u.y);
+    return __builtin_bit_cast(s16x4, x);
+}
+// fp32 -> bf16 by truncation; exact for values that are bf16 already.
+__device__ __forceinline__ s16x4 trunc_bf16x4(const f32x4& t) {
+    uint2 r;
+    r.x = (__float_as_uint(t[0]) >> 16) | (__float_as_uint(t[1]) & 0xFFFF0000u);
+    r.y = (__float_as_uint(t[2]) >> 16) | (__float_as_uint(t[3]) & 0xFFFF0000u);
+    return __builtin_bit_cast(s16x4, r);
+}
+
+struct DecodeArgs {
+    const uint16_t* q_row;  // [2560] of this slot
+    uint32_t limit;
+    const uint32_t* pt;
+    uint16_t* pool;
+    float* rec;       // this slot's records: [16][rec_stride][130]
+    uint32_t rec_stride;
+    uint16_t* out;    // this slot: [2048]
+};
+
+
+// 256 threads process chunks [c_first, c_end) of one (slot, kv head) as ONE
+// range: every wave keeps a single online-softmax state across all chunks of
+// the range, the 4 wave states are folded once at the end and written as one
+// record {m, l, acc[128]} per query head at rec[(qh * rec_stride + group)],
+// or, when the range is the only one (nvalid <= cpw), as the output
+// bf16(acc / l). With KV2 the workgroup has 512 threads and threads 256-511
+// run the same body for the second KV head over the same chunks (own LDS).
+// Waves take tiles j = wave, wave+4, ... of each chunk (a chunk still bounds
+// the tile grid, so with cpw = 1 a record is exactly the chunk partial of
+// the reference's chunk kernel); the next tile's loads are issued before the
+// current tile computes, also across chunk boundaries. cpw > 1 requires
+// C % 64 == 0.
+template <bool PH0, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P>
+__device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t layer,
+                                                  DevLayout ly, uint32_t NC,
+                                                  const float* __restrict__ inv_freq,
+                                                  uint32_t C, uint32_t kvh, uint32_t group,
+                                                  uint32_t cpw) {
+    constexpr uint32_t NH = KV2 ? 2u : 1u;  // kv heads per workgroup
+    const uint32_t half = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : 0u;
+    // Load layouts per chunk tier. ROWS (64-position tier): K and V as whole
+    // head rows, both transposed through LDS (measured faster for 2K
+    // contexts). VROWS (all tiers of the straight-line schedule): V as head
+    // rows read back with the transposing LDS read, K in operand layout
+    // (row-loading K too measured equal at C = 256). The generic schedule
+    // keeps both in operand layout.
+    constexpr bool ROWS = TPW == 1u;
+    constexpr bool VROWS = TPW >= 1u;
+    __shared__ __align__(16) uint16_t s_q_[NH][PH0 ? kGroup * kD : 1];  // rotated q rows
+    __shared__ __align__(16) uint16_t s_fresh_[NH][256];  // K | V of `limit`
+    __shared__ uint32_t s_pages_[NH][kPageCache];         // page ids of this block's range
+    // per wave: K and V tile, 16 x 256 B (row loads only)
+    __shared__ uint4 s_x_[NH][VROWS ? kWaves : 1u][VROWS ? 2u * 16u * 16u : 1u];
+    __shared__ float s_m_[NH][kWaves][kGroup], s_l_[NH][kWaves][kGroup];
+    __shared__ __align__(16) float s_acc_[NH][kWaves][kGroup][kD];
+    auto& s_q = s_q_[half];
+    auto& s_fresh = s_fresh_[half];
+    auto& s_pages = s_pages_[half];
+    auto& s_x = s_x_[half];
+    auto& s_m = s_m_[half];
+    auto& s_l = s_l_[half];
+    auto& s_acc = s_acc_[half];
+
+    const uint32_t limit = a.limit;
+    const uint32_t nvalid = min(limit / C + 1u, NC);
+    const uint32_t c_first = group * cpw;
+    if (c_first >= nvalid) return;  // uniform over the block
+    const uint32_t c_end = min(c_first + cpw, nvalid);
+    const bool direct = nvalid <= cpw;  // the only range: write the output
+    const uint32_t tid = threadIdx.x & 255u;
+    // Wave index made provably wave-uniform so every tile / chunk decision
+    // below compiles to scalar branches.
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t lane = tid & 63u;
+    const uint32_t tok = lane & 15u;  // row within a 16-position tile / head col
+    const uint32_t grp = lane >> 4;   // 0..3
+
+    const uint16_t* __restrict__ q_row = a.q_row;
+    const uint32_t* __restrict__ pt = a.pt;
+    uint16_t* __restrict__ pool = a.pool;
+    const uint32_t kvcol = kvh * kD + 8u * grp;  // within a token's K or V half
+
+    // Position `limit` is kept out of the streamed tiles and added as one extra
+    // tile from LDS by wave 0 of the owning block: with phase0 its K/V come
+    // from the qkv row, otherwise from the pool. Both modes therefore run the
+    // same arithmetic (phase0 output == append-then-attend output, bitwise) and
+    // the streaming loop never patches registers.
+    const uint32_t last_pos = limit - 1u;  // last streamed position
+    auto chunk_end = [&](uint32_t c) { return min(c * C + C - 1u, last_pos); };
+    auto chunk_tiles = [&](uint32_t c) {
+        const uint32_t cs = c * C;
+        return (limit == 0u || last_pos < cs) ? 0u : (chunk_end(c) - cs) / kTile + 1u;
+    };
+    // A 16-position tile starts 16-aligned, so with P >= 16 (PAGE16) it lies in
+    // one page and the page id is wave-uniform: it is read through the scalar
+    // path and does not serialize behind the vector loads in flight.
+    // Page ids of the block's position range, staged once into LDS (read by
+    // all tiles with a short LDS latency instead of a scalar-cache miss in
+    // front of every tile's loads).
+    const uint32_t page0 = (c_first * C) >> ly.log2p;
+    const uint32_t npages_rng = ((min(c_end * C, limit + 1u) - 1u) >> ly.log2p) - page0 + 1u;
+    const bool cached_pages = PAGE16 && npages_rng <= kPageCache;
+    // `direct` reads the page id from the table itself (scalar path for
+    // PAGE16) instead of the LDS copy; the first tiles use it so that they
+    // do not wait for the staging barrier.
+    auto load_tile = [&](Tile& T, uint32_t c, uint32_t j, bool from_table) {
+        const uint32_t t0 = c * C + j * kTile;
+        if constexpr (ROWS) {
+            // Row loads: lane (q = lane/16, x = lane%16) reads the 16-byte chunk x
+            // of the K and V head rows of tokens t0 + q + 4r (r < 4), so every 16
+            // lanes read one whole 256-byte head row (whole 128-byte lines per
+            // request). xpose() restores the MFMA operand layout through LDS.
+            const uint32_t cend = chunk_end(c);
+            uint32_t page_u = 0;
+            if (PAGE16 && cached_pages && !from_table)
+                page_u = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
+            else if constexpr (PAGE16)
+                page_u = ((const __attribute__((address_space(4))) uint32_t*)(pt))
+                    [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t p = min(t0 + grp + 4u * r, cend);
+                const uint32_t page = PAGE16 ? page_u : pt[p >> ly.log2p];
+                const uint16_t* src =
+                    pool + token_base(ly, layer, page, p & ly.pmask) + kvh * kD + 8u * tok;
+                T.k[r] = ld16(src);
+                T.v[r] = ld16(src + 256u);
+            }
+            return;
+        }
+        const uint32_t p = min(t0 + tok, chunk_end(c));
+        uint32_t page;
+        if (PAGE16 && cached_pages && !from_table)
+            page = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
+        else if constexpr (PAGE16)
+            page = ((const __attribute__((address_space(4))) uint32_t*)(pt))
+                [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)];
+        else
+            page = pt[p >> ly.log2p];
+        const uint16_t* src = pool + token_base(ly, layer, page, p & ly.pmask) + kvcol;
+        if constexpr (VROWS) {  // K in operand layout, V as row loads
+            const uint32_t cend = chunk_end(c);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) T.k[m] = ld16(src + 32u * m);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t pr = min(t0 + grp + 4u * r, cend);
+                const uint32_t pg = PAGE16 ? page : pt[pr >> ly.log2p];
+                T.v[r] = ld16(pool + token_base(ly, layer, pg, pr & ly.pmask) + 256u +
+                              kvh * kD + 8u * tok);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                T.k[m] = ld16(src + 32u * m);
+                T.v[m] = ld16(src + 256u + 32u * m);
+            }
+        }
+    };
+    // Row-loaded tile -> operand layout (lane (row, group) holds dims
+    // [32m + 8*group, +8) of token row, m < 4) through this wave's LDS tile:
+    // chunk x of token t is stored at slot x ^ t of row t, so both the stores
+    // (16 chunks of 4 rows per instruction) and the operand reads (one chunk
+    // of 16 rows per lane group) spread over all LDS banks. A wave reads only
+    // what it wrote, in order: no barrier is needed.
+    auto xpose = [&](const Tile& T) -> Tile {
+        if constexpr (!VROWS) return T;
+        uint4* xs = s_x[wave];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t t = grp + 4u * r;
+            if constexpr (ROWS) xs[t * 16u + (tok ^ t)] = T.k[r];
+            xs[256u + t * 16u + (tok ^ t)] = T.v[r];
+        }
+        __builtin_amdgcn_wave_barrier();
+        Tile O;
+        // V^T operands with the transposing LDS read: within each 16-lane
+        // group, ds_read_b64_tr_b16 gives lane x the element x%4 of the 8-byte
+        // rows addressed by lanes 4j + x/4 (j < 4). Lane 4j + a of group grp
+        // addresses token 4*grp + j, dims 32m + 8a + 4h, so lane x receives
+        // dim 32m + 8(x/4) + 4h + x%4 of tokens 4*grp + j: the A operand of
+        // O^T += V^T x P^T with the same dim order the accumulator uses.
+        const uint32_t vt_tok = 4u * grp + (tok >> 2);
+        const uint16_t* vs = reinterpret_cast<const uint16_t*>(xs + 256u) + vt_tok * 128u;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t x = (4u * m + grp) ^ tok;
+            O.k[m] = ROWS ? xs[tok * 16u + x] : T.k[m];
+            const uint16_t* vr = vs + (((4u * m + (tok & 3u)) ^ vt_tok) * 8u);
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(vr));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(vr + 4));
+            const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+            O.v[m] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+        }
+        __builtin_amdgcn_wave_barrier();
+        return O;
+    };
+    // Next (chunk, tile) of this wave after (c, j); false past the range.
+    auto advance = [&](uint32_t& c, uint32_t& j) {
+        j += kWaves;
+        while (c < c_end && j >= chunk_tiles(c)) {
+            ++c;
+            j = wave;
+        }
+        return c < c_end;
+    };
+    // Straight-line schedule helper: tile i (0..TPW-1) of this wave in chunk
+    // c, clamped to an existing tile past the end of the range (the clamped
+    // load re-reads a tile and is never accumulated).
+    auto clamp_load = [&](Tile& T, uint32_t c, uint32_t i, bool from_table) {
+        const uint32_t cl = c < c_end ? c : c_end - 1u;
+        const uint32_t nt = chunk_tiles(cl);
+        uint32_t j = wave + 4u * i;
+        if (c >= c_end) j = wave + 4u * (TPW - 1u);
+        if (nt == 0u) j = 0u;
+        else if (j >= nt) j = nt - 1u;
+        load_tile(T, cl, j, from_table);
+    };
+
+    // Start-up, ordered for latency: (a) loads that need nothing computed
+    // (q, inv_freq, the new token's k/v), (b) the block's page ids, (c) the
+    // first K/V tiles (one dependent scalar load after `limit`), and only
+    // then (d) the work that waits for (a) and (b). Phase0: cos/sin of
+    // position `limit`; the block owning `limit` builds the rotated K and the
+    // V of that token in LDS and stores both to the pool.
+    const bool owner = limit / C < c_end && limit < NC * C;
+    const bool real = tok < kGroup;
+    // All start-up loads are unconditional (addresses clamped) so that no
+    // divergent branch makes the compiler wait for them before the first
+    // K/V tiles are issued.
+    // q: without phase0 each lane loads its Q^T operand directly; with phase0
+    // thread tid loads dims p and p + 64 (p = tid % 64) of heads 2w, 2w + 1
+    // (w = tid / 64) of this KV head, rotates them with pair p and stages the
+    // rotated rows in LDS (4 rotations per thread instead of 32 per lane).
+    uint4 qr[4];
+    uint16_t qx[2][2];  // phase0: [head 2w + hh][dim p, p + 64]
+    if constexpr (!PH0) {
+        const uint16_t* qsrc = q_row + (kvh * kGroup + (real ? tok : 0u)) * kD + 8u * grp;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) qr[m] = *reinterpret_cast<const uint4*>(qsrc + 32u * m);
+    } else {
+        const uint16_t* qh0 = q_row + (kvh * kGroup + 2u * wave) * kD + (tid & 63u);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            qx[hh][0] = qh0[hh * kD];
+            qx[hh][1] = qh0[hh * kD + 64u];
+        }
+    }
+    const uint32_t t64 = tid & 63u;
+    float invf = 0.f;
+    uint16_t kx = 0, kx2 = 0;
+    uint32_t fresh_v = 0u;
+    uint2 fresh_kv = make_uint2(0u, 0u);
+    const uint32_t limit_page =
+        owner ? ((const __attribute__((address_space(4))) uint32_t*)(pt))[limit >> ly.log2p]
+              : 0u;
+    if (PH0) {  // every block reads the new token's k/v (a few cached bytes)
+        invf = inv_freq[t64];
+        const uint16_t* kr = q_row + kKCol + kvh * kD;
+        kx = kr[t64];
+        kx2 = kr[t64 + 64u];
+        fresh_v = *reinterpret_cast<const uint32_t*>(q_row + kVCol + kvh * kD + 2u * t64);
+    } else if (owner) {  // K|V of `limit` from the pool, 32 lanes per half
+        const uint16_t* src =
+            pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
+        fresh_kv = *reinterpret_cast<const uint2*>(src + 256u * (t64 >> 5) + (t64 & 31u) * 4u);
+    }
+    uint32_t staged_page = 0u;
+    if (cached_pages) staged_page = pt[page0 + min(tid, npages_rng - 1u)];
+
+    constexpr uint32_t RING = kRing;
+    Tile R[RING];
+    Tile& A = R[0];
+    Tile& B = R[RING > 1u ? 1u : 0u];
+    uint32_t ac = c_first, aj = wave;
+    bool a_ok = false;
+    if constexpr (TPW > 0) {
+#pragma unroll
+        for (uint32_t g = 0; g + 1u < RING; ++g)
+            clamp_load(R[g], c_first + g / TPW, g % TPW, true);
+    } else {
+        a_ok = wave < chunk_tiles(c_first) || advance(ac, aj);
+        if (a_ok) load_tile(A, ac, aj, true);
+    }
+
+    if (cached_pages && tid < npages_rng) s_pages[tid] = staged_page;
+    if (PH0) {
+        // cos/sin of pair p = tid % 64 (every wave evaluates the same 64)
+        float c, sn;
+        rope_sincos((float)limit * invf, &c, &sn);
+        const uint32_t p = tid & 63u;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const float x = bf16_to_f32(qx[hh][0]), x2 = bf16_to_f32(qx[hh][1]);
+            uint16_t* qd = &s_q[(2u * wave + hh) * kD + p];
+            qd[0] = f32_to_bf16(rope_rotate(x, x2, c, sn, true));
+            qd[64] = f32_to_bf16(rope_rotate(x2, x, c, sn, false));
+        }
+        if (owner && tid < 64u) {  // pair tid rotates dims tid and tid + 64 of k
+            const float x = bf16_to_f32(kx), x2 = bf16_to_f32(kx2);
+            const uint16_t lo = f32_to_bf16(rope_rotate(x, x2, c, sn, true));
+            const uint16_t hi = f32_to_bf16(rope_rotate(x2, x, c, sn, false));
+            s_fresh[tid] = lo;
+            s_fresh[tid + 64u] = hi;
+            *reinterpret_cast<uint32_t*>(&s_fresh[128u + 2u * tid]) = fresh_v;
+            uint16_t* dst =
+                pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
+            dst[tid] = lo;
+            dst[tid + 64u] = hi;
+            *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = fresh_v;
+        }
+    } else if (owner && tid < 64u) {
+        const uint32_t h = tid >> 5, d = (tid & 31u) * 4u;
+        *reinterpret_cast<uint2*>(&s_fresh[128u * h + d]) = fresh_kv;
+    }
+    __syncthreads();
+
+    // Q^T B operand: lane holds q[head = tok][32m + 8*grp + i]; heads >= 8 zero.
+    bf16x8 qb[4];
+    if constexpr (PH0) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            qr[m] = *reinterpret_cast<const uint4*>(
+                &s_q[(real ? tok : 0u) * kD + 32u * m + 8u * grp]);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) qb[m] = as_bf16x8(real ? qr[m] : make_uint4(0u, 0u, 0u, 0u));
+
+    // Identity B operand for the transpose: B[k][c] = (k == c), k = 4*grp + i.
+    s16x4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        ident[i] = (4u * grp + (uint32_t)i == tok) ? (short)0x3F80 : (short)0;
+
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[m][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Accumulates the tile starting at position `tstart` (rows after `tend`
+    // masked) into the wave's state.
+    auto accumulate = [&](const Tile& T, uint32_t tstart, uint32_t tend) {
+        // S^T = K x Q^T
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[m]), qb[m], s, 0, 0, 0);
+        const uint32_t pos0 = tstart + 4u * grp;
+        float sc[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            float v;
+            {
+#pragma clang fp contract(off)
+                v = s[jj] * kScoreScale;
+            }
+            sc[jj] = (pos0 + (uint32_t)jj <= tend) ? v : -INFINITY;
+        }
+        float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        tm = swap32_max(swap16_max(tm));
+        const float mn = fmaxf(m_run, tm);
+        const float renew = (m_run == -INFINITY) ? 0.f : __expf(m_run - mn);
+        float p[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) p[jj] = __expf(sc[jj] - mn);
+        float ls = (p[0] + p[1]) + (p[2] + p[3]);
+        ls = swap32_sum(swap16_sum(ls));
+        l_run = l_run * renew + ls;
+        m_run = mn;
+        s16x4 pb;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) pb[jj] = (short)f32_to_bf16(p[jj]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                s16x4 vop;
+                if constexpr (VROWS) {  // T.v already holds the V^T operands
+                    vop = half_s16x4(T.v[m], h);
+                } else {
+                    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    vop = trunc_bf16x4(__builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                        half_s16x4(T.v[m], h), ident, z, 0, 0, 0));
+                }
+                acc[m][h] = acc[m][h] * renew;
+                if constexpr (FP32P) {
+                    // fp32 P: four 16x16x4 fp32 MFMAs contract the positions
+                    // {4g + i : g < 4} for i = 0..3. Lane (dim row r, g) holds
+                    // V^T[r][4g + i] as element i of its V^T operand and
+                    // P^T[4g + i][head] as p[i]; the output layout is the one
+                    // of the bf16 16x16x16 product.
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[m][h] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            bf16_to_f32((uint16_t)vop[i]), p[i], acc[m][h], 0, 0, 0);
+                } else {
+                    acc[m][h] =
+                        __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vop, pb, acc[m][h], 0, 0, 0);
+                }
+            }
+    };
+
+    if constexpr (TPW > 0) {
+        // Straight-line schedule (C == 64 * TPW): wave w owns tiles
+        // j = w + 4i, i < TPW, of every chunk. Chunks are walked with the tile
+        // loop fully unrolled, so the ring slot of every tile is a
+        // compile-time constant and the load of the next tile is issued
+        // before the current one computes; the wait before each compute then
+        // covers only the older load group. Loads for chunks past the range
+        // are skipped (scalar branch; the compiler's wait counts stay
+        // conservative across it), tiles past a chunk's end within the range
+        // are clamped to an already-fetched tile and never accumulated.
+        // U chunks are unrolled per loop trip so that U * TPW is a multiple
+        // of the ring size and every slot index is a compile-time constant.
+        constexpr uint32_t U = (TPW % RING == 0u) ? 1u : RING;
+        static_assert((U * TPW) % RING == 0u, "ring slots must repeat per loop trip");
+        for (uint32_t c = c_first; c < c_end; c += U) {
+#pragma clang loop unroll(full)
+            for (uint32_t h = 0; h < U; ++h) {
+                const uint32_t cc2 = c + h;
+#pragma clang loop unroll(full)
+                for (uint32_t i = 0; i < TPW; ++i) {
+                    const uint32_t g = h * TPW + i;
+                    const uint32_t ga = g + RING - 1u;  // tile to prefetch
+                    if (c + ga / TPW < c_end)
+                        clamp_load(R[ga % RING], c + ga / TPW, ga % TPW, false);
+                    const uint32_t j = wave + 4u * i;
+                    if (cc2 < c_end && j < chunk_tiles(cc2))
+                        accumulate(xpose(R[g % RING]), cc2 * C + j * kTile, chunk_end(cc2));
+                }
+            }
+        }
+    } else {
+        // Generic schedule (any C multiple of 16): ping-pong over two tiles.
+        while (a_ok) {
+            uint32_t bc = ac, bj = aj;
+            const bool b_ok = advance(bc, bj);
+            if (b_ok) load_tile(B, bc, bj, false);
+            accumulate(xpose(A), ac * C + aj * kTile, chunk_end(ac));
+            if (!b_ok) break;
+            uint32_t nc = bc, nj = bj;
+            a_ok = advance(nc, nj);
+            if (a_ok) load_tile(A, nc, nj, false);
+            accumulate(xpose(B), bc * C + bj * kTile, chunk_end(bc));
+            ac = nc;
+            aj = nj;
+        }
+    }
+    if (owner && wave == 0u) {  // position `limit` from LDS
+        Tile F;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            F.k[m] = *reinterpret_cast<const uint4*>(&s_fresh[32u * m + 8u * grp]);
+            if constexpr (VROWS) {  // V^T operand: dim d of the token in every k slot
+                uint32_t w[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t d = 32u * m + 8u * (tok >> 2) + 4u * h + (tok & 3u);
+                    w[h] = (uint32_t)s_fresh[128u + d] * 0x10001u;
+                }
+                F.v[m] = make_uint4(w[0], w[0], w[1], w[1]);
+            } else {
+                F.v[m] = *reinterpret_cast<const uint4*>(&s_fresh[128u + 32u * m + 8u * grp]);
+            }
+        }
+        accumulate(F, limit, limit);
+    }
+
+    // Fold the 4 wave states in fixed wave order and write the record (or
+    // the output).
+    if (tok < kGroup) {
+        if (grp == 0u) {
+            s_m[wave][tok] = m_run;
+            s_l[wave][tok] = l_run;
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                *reinterpret_cast<f32x4*>(&s_acc[wave][tok][32u * m + 8u * grp + 4u * h]) =
+                    acc[m][h];
+    }
+    __syncthreads();
+    const uint32_t head = tid >> 5;        // 0..7
+    const uint32_t d4 = (tid & 31u) * 4u;  // 4 dims
+    const uint32_t qh = kvh * kGroup + head;
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w)
+        if (s_l[w][head] != 0.f) M = fmaxf(M, s_m[w][head]);
+    float L = 0.f;
+    f32x4 Acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) {
+        const float lw = s_l[w][head];
+        if (lw == 0.f) continue;
+        const float f = __expf(s_m[w][head] - M);
+        L += lw * f;
+        Acc += *reinterpret_cast<const f32x4*>(&s_acc[w][head][d4]) * f;
+    }
+    if (direct) {
+        uint16_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = f32_to_bf16(L > 0.f ? Acc[i] / L : 0.f);
+        *reinterpret_cast<uint2*>(a.out + qh * kD + d4) =
+            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
+                       (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+        return;
+    }
+    float* pw = a.rec + ((size_t)qh * a.rec_stride + group) * kPartial;
+    if (d4 == 0u) *reinterpret_cast<float2*>(pw) = make_float2(M, L);
+    *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(Acc[0], Acc[1]);
+    *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(Acc[2], Acc[3]);
+}
+
+// ---- merge of the decode records ----
+constexpr uint32_t kMergeTasks = 64;  // 16 heads x 4 dim slices of 32
+constexpr uint32_t kMaxRanges = 256;  // records per head merge_task folds
+
+// One merge task on 256 threads (t = thread index within them): thread
+// (record lane rl = t / 8, dim quad t % 8) folds records rl, rl + 32, ...
+// (ascending), then the 32 record lanes are combined by a fixed tree
+// (xor-shuffles 8, 16, 32 within a wave, then waves 0..3 in order).
+// out = bf16(A / L) with M = max m over records with l != 0,
+// f = exp(m - M), L = sum l f, A = sum acc f (the reference merge rule).
+__device__ __forceinline__ void merge_task(const float* __restrict__ rec, uint32_t stride,
+                                           uint32_t nr, uint32_t task, uint16_t* out,
+                                           uint32_t t, float* s_red /* [4 + 4*8*5] */) {
+    const uint32_t head = task >> 2;
+    const uint32_t d = (task & 3u) * 32u + (t & 7u) * 4u;
+    const uint32_t rl = t >> 3;
+    const uint32_t w = t >> 6;
+    const float* base = rec + (size_t)head * stride * kPartial;
+    constexpr uint32_t kPer = kMaxRanges / 32u;  // records per thread
+    float2 ml[kPer], a01[kPer], a23[kPer];
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        const uint32_t r = rl + 32u * i;
+        const float* p = base + (size_t)(r < nr ? r : 0u) * kPartial;
+        if (32u * i < nr) {  // uniform: some lane of the loop trip has a record
+            ml[i] = *reinterpret_cast<const float2*>(p);
+            a01[i] = *reinterpret_cast<const float2*>(p + 2 + d);
+            a23[i] = *reinterpret_cast<const float2*>(p + 4 + d);
+        } else {
+            ml[i] = make_float2(0.f, 0.f);
+            a01[i] = a23[i] = make_float2(0.f, 0.f);
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i)
+        if (rl + 32u * i < nr && ml[i].y != 0.f) mx = fmaxf(mx, ml[i].x);
+    mx = wave_max(mx);
+    if ((t & 63u) == 0u) s_red[w] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        if (rl + 32u * i < nr && ml[i].y != 0.f) {
+            const float f = expf(ml[i].x - M);
+            L += ml[i].y * f;
+            A += f32x4{a01[i].x, a01[i].y, a23[i].x, a23[i].y} * f;
+        }
+    }
+#pragma unroll
+    for (int x = 8; x <= 32; x <<= 1) {
+        L += __shfl_xor(L, x);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) A[k] += __shfl_xor(A[k], x);
+    }
+    float* s_w = s_red + 4;  // [4 waves][8 quads][5]
+    if ((t & 63u) < 8u) {
+        float* q = s_w + (w * 8u + (t & 7u)) * 5u;
+        q[0] = L;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[1 + k] = A[k];
+    }
+    __syncthreads();
+    if (t < 8u) {
+        float Lt = 0.f;
+        f32x4 At = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t ww = 0; ww < 4u; ++ww) {
+            const float* q = s_w + (ww * 8u + t) * 5u;
+            Lt += q[0];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) At[k] += q[1 + k];
+        }
+        uint16_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = f32_to_bf16(Lt > 0.f ? At[k] / Lt : 0.f);
+        *reinterpret_cast<uint2*>(out + head * kD + d) =
+            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
+                       (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+    }
+    __syncthreads();  // s_red is reused by the next task
+}
+
+__device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
+                                                   uint32_t NC) {
+    const uint32_t n = limit / C + 1u;
+    return n > NC ? NC : n;
+}
+
+// grid = (ceil(NC / cpw), 2 kv heads (1 with KV2), B slots). Single-session
+// launches pass B = 1 and the direct pointers; batched launches resolve
+// per-slot pointers from device tables. Records of slot s start at
+// partials + s * 16 * rec_stride * 130 with a per-head stride of rec_stride
+// records (rec_stride >= the number of ranges, ceil(NC / cpw)).
+template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P>
+__global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
+    __attribute__((amdgpu_waves_per_eu(2))) decode_chunk_kernel(
+    const uint16_t* __restrict__ q_rows, const uint32_t* d_pos,
+    const uint32_t* const* __restrict__ slot_pos, uint32_t layer,
+    const uint32_t* pt, const uint32_t* const* __restrict__ slot_pt,
+    uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
+    float* __restrict__ partials, uint32_t NC, uint32_t rec_stride, uint16_t* __restrict__ out,
+    const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw) {
+    uint32_t slot = blockIdx.z, group = blockIdx.x, limit;
+    if constexpr (BATCH) {
+        // Work compaction: the (x, slot) workgroups are numbered densely over
+        // the chunk groups that exist (slot by slot, ascending), so ragged
+        // slots leave their idle workgroups at the end of the grid instead of
+        // between the working ones. Every wave derives the same mapping from
+        // all slots' limits: lane s reads slot s's limit, a DPP scan gives
+        // the running total of chunk groups, and the slot is the first one
+        // whose total exceeds this workgroup's index.
+        const uint32_t B = gridDim.z;
+        const uint32_t flat = blockIdx.x + gridDim.x * blockIdx.z;
+        const uint32_t Cc = TPW > 0u ? 64u * TPW : C;  // 64 * TPW: a shift
+        const bool cpw_pow2 = (cpw & (cpw - 1u)) == 0u;
+        const uint32_t cpw_log2 = (uint32_t)__builtin_ctz(cpw);
+        auto groups = [&](uint32_t nv) {
+            return cpw_pow2 ? (nv + cpw - 1u) >> cpw_log2 : (nv + cpw - 1u) / cpw;
+        };
+        {
+            const uint32_t lane = threadIdx.x & 63u;
+            uint32_t lim = 0u, cnt = 0u;
+            if (lane < B) {
+                lim = *slot_pos[lane];
+                cnt = groups(n_valid_chunks(lim, Cc, NC));
+            }
+            // inclusive scan over the 64 lanes: row_shr 1, 2, 4, 8 within each
+            // 16-lane row, then row_bcast 15 (into rows 1, 3) and 31 (rows 2, 3)
+            uint32_t incl = cnt;
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x111, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x112, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x114, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x118, 0xF, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x142, 0xA, 0xF, false);
+            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x143, 0xC, 0xF, false);
+            slot = (uint32_t)__builtin_popcountll(
+                __builtin_amdgcn_ballot_w64(lane < B && incl <= flat));
+            if (slot < B) {
+                const uint32_t end = (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)slot);
+                const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)cnt, (int)slot);
+                group = flat - (end - c);
+                limit = (uint32_t)__builtin_amdgcn_readlane((int)lim, (int)slot);
+            }
+        }
+        if (slot >= B) return;  // past the last existing chunk group (uniform)
+    } else {
+        limit = *d_pos;
+    }
+    DecodeArgs a;
+    a.q_row = q_rows + (size_t)slot * kRow;
+    a.limit = limit;
+    a.pt = BATCH ? slot_pt[slot] : pt;
+    a.pool = BATCH ? slot_kv[slot] : pool;
+    a.rec = partials + (size_t)slot * kHq * rec_stride * kPartial;
+    a.rec_stride = rec_stride;
+    a.out = out + (size_t)slot * kHq * kD;
+    const uint32_t kvh = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : blockIdx.y;
+    decode_range_body<PH0, PAGE16, TPW, KV2, FP32P>(a, layer, ly, NC, inv_freq, C, kvh, group,
+                                                    cpw);
+}
+
+}  // namespace
+
+// One chunk-kernel launch (records, or the output when there is one range).
+struct ChunkLaunch {
+    const uint16_t* q;
+    const uint32_t* d_pos;
+    const uint32_t* const* slot_pos;
+    uint32_t B;
+    uint32_t layer;
+    const uint32_t* pt;
+    const uint32_t* const* slot_pt;
+    uint16_t* pool;
+    uint16_t* const* slot_kv;
+    DevLayout ly;
+    float* partials;
+    uint32_t NC;
+    uint32_t rec_stride;
+    uint16_t* out;
+    hipStream_t st;
+    const float* inv_freq;
+    uint32_t C;
+    uint32_t cpw;
+    bool batched;
+};
+
+// Both KV heads in one 512-thread workgroup when that still gives every CU a
+// workgroup: the 8 waves of a CU then stream the same token rows at the same
+// pace (two independent workgroups per CU finish several us apart, and the
+// later one runs alone at half the loads in flight). Batched launches keep
+// one head per workgroup: their ragged slots leave many workgroups short,
+// and finer ones balance better (measured).
+inline bool use_kv2(const ChunkLaunch& L) {
+    const uint32_t nx = (L.NC + L.cpw - 1u) / L.cpw;
+    return !L.batched && (L.C == 256u || L.C == 512u) && nx >= kKv2MinBlocks;
+}
+
+template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P>
+void launch_one(const ChunkLaunch& L) {
+    const uint32_t nx = (L.NC + L.cpw - 1u) / L.cpw;
+    const dim3 grid(nx, KV2 ? 1u : kHkv, L.B);
+    const dim3 block(KV2 ? kHkv * kThreads : kThreads);
+    hipLaunchKernelGGL((decode_chunk_kernel<PH0, BATCH, PAGE16, TPW, KV2, FP32P>), grid, block,
+                       0, L.st, L.q, L.d_pos, L.slot_pos, L.layer, L.pt, L.slot_pt, L.pool,
+                       L.slot_kv, L.ly, L.partials, L.NC, L.rec_stride, L.out, L.inv_freq, L.C,
+                       L.cpw);
+}
+
+template <bool PH0, bool BATCH, bool PAGE16, bool FP32P>
+void launch_tiers(const ChunkLaunch& L) {
+    bool kv2 = false;
+    if constexpr (!BATCH) kv2 = use_kv2(L);
+    switch (L.C) {
+        case 64: launch_one<PH0, BATCH, PAGE16, 1u, false, FP32P>(L); break;
+        case 128: launch_one<PH0, BATCH, PAGE16, 2u, false, FP32P>(L); break;
+        case 256:
+            if constexpr (!BATCH)
+                if (kv2) { launch_one<PH0, BATCH, PAGE16, 4u, true, FP32P>(L); break; }
+            launch_one<PH0, BATCH, PAGE16, 4u, false, FP32P>(L);
+            break;
+        case 512:
+            if constexpr (!BATCH)
+                if (kv2) { launch_one<PH0, BATCH, PAGE16, 8u, true, FP32P>(L); break; }
+            launch_one<PH0, BATCH, PAGE16, 8u, false, FP32P>(L);
+            break;
+        default: launch_one<PH0, BATCH, PAGE16, 0u, false, FP32P>(L); break;
+    }
+}
+
+// Launches the chunk kernel of L (instantiated once per P.V precision, each in
+// its own translation unit).
+template <bool FP32P>
+mc_status_t launch_chunk_kernel(const ChunkLaunch& L) {
+    const bool page16 = L.ly.log2p >= 4u;
+    const bool ph0 = L.inv_freq != nullptr;
+    if (L.batched) {
+        if (ph0) {
+            if (page16) launch_tiers<true, true, true, FP32P>(L);
+            else launch_tiers<true, true, false, FP32P>(L);
+        } else {
+            if (page16) launch_tiers<false, true, true, FP32P>(L);
+            else launch_tiers<false, true, false, FP32P>(L);
+        }
+    } else {
+        if (ph0) {
+            if (page16) launch_tiers<true, false, true, FP32P>(L);
+            else launch_tiers<true, false, false, FP32P>(L);
+        } else {
+            if (page16) launch_tiers<false, false, true, FP32P>(L);
+            else launch_tiers<false, false, false, FP32P>(L);
+        }
+    }
+    return check_launch("decode attention launch failed");
+}
+
+extern template mc_status_t launch_chunk_kernel<false>(const ChunkLaunch&);
+extern template mc_status_t launch_chunk_kernel<true>(const ChunkLaunch&);
+
+}  // namespace mckv

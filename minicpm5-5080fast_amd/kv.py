@@ -163,6 +163,29 @@ def debug_prefill_packing(enable: bool) -> bool:
     return bool(prev.value)
 
 
+def debug_prefill_status(reset: bool = False) -> int:
+    """Number of two-half prefill barrier waits that ran out of their bound on
+    the current device since the last reset (non-zero means a prefill output
+    may be wrong); `reset` clears the count after reading. Synchronous.
+    Debug hook, no reference counterpart."""
+    n = C.c_uint32(0)
+    check(lib().mc_kv_debug_prefill_status(C.byref(n), 1 if reset else 0),
+          "debug_prefill_status")
+    return n.value
+
+
+DECODE_FP32P_FROM_ENV = 0xFFFFFFFF
+
+
+def debug_decode_fp32p(fp32_p: int) -> int:
+    """Sets the decode P.V precision (0 = bf16 P, 1 = fp32 P,
+    DECODE_FP32P_FROM_ENV = MC_ATTN_HMMA_OFF) and returns the previous
+    setting. Debug hook (the reference selects fp32 P by environment only)."""
+    prev = C.c_uint32(0)
+    check(lib().mc_kv_debug_decode_fp32p(fp32_p, C.byref(prev)), "debug_decode_fp32p")
+    return prev.value
+
+
 def launch_decode_advance(d_seq, d_next_token, d_seq_len, stream=None) -> None:
     check(lib().mc_kv_decode_advance(_ptr(d_seq), _ptr(d_next_token), _ptr(d_seq_len),
                                      _stream(stream)), "launch_decode_advance")

@@ -47,6 +47,7 @@ def lib():
         L.orc_rope_append.argtypes = [P, u32, u32, u32, P, u32, u32, dbl, i32, P, P]
         L.orc_attn_ref.argtypes = [P, u32, u32, u32, P, P, u32, u32, P, i32]
         L.orc_decode_chunks.argtypes = [P, u32, u32, P, P, u32, u32, u32, u32, P, P]
+        L.orc_decode_chunks_p.argtypes = [P, u32, u32, P, P, u32, u32, u32, u32, P, P, i32]
         L.orc_merge2.argtypes = [P, u32, u32, P, P]
         L.orc_decode_cpu_mt.argtypes = [P, P, P, P, u32, u32, u32, u32, P, i32]
         _LIB = L
@@ -189,12 +190,15 @@ def attn_ref(q_rows, tokens, base_pos, layer, pool, pt, P, maxp, threads=None):
     return out
 
 
-def decode_chunks(q_row, limit, layer, pool, pt, P, maxp, C_, NC):
+def decode_chunks(q_row, limit, layer, pool, pt, P, maxp, C_, NC, fp32_p=False):
+    """Per-chunk partials [16][NC][130] (and the direct output when
+    limit < C_); fp32_p selects fp32 P in P.V instead of bf16-rounded P."""
     parts = np.full((16, NC, PSTRIDE), np.nan, dtype=np.float32)
     out = np.zeros(2048, dtype=np.uint16)
     pt = np.ascontiguousarray(pt, dtype=np.uint32)
-    lib().orc_decode_chunks(_p(np.ascontiguousarray(q_row)), limit, layer, _p(pool),
-                            _p(pt), P, maxp, C_, NC, _p(parts), _p(out))
+    lib().orc_decode_chunks_p(_p(np.ascontiguousarray(q_row)), limit, layer, _p(pool),
+                              _p(pt), P, maxp, C_, NC, _p(parts), _p(out),
+                              1 if fp32_p else 0)
     return parts, out
 
 

@@ -231,12 +231,14 @@ void orc_attn_ref(const uint16_t* q_rows, uint32_t tokens, uint32_t base_pos,
 /* ---- chunked decode with bf16 P (native/tests/kernel_ops.cpp:2912-2974
  * h2_cpu_ref, the CPU statement of attn_kv_kernel_h, attention_decode.cu:
  * 966-1368): per (qh, chunk c) a single 16-position-batch online softmax in
- * fp32; l accumulates fp32 p, acc accumulates bf16-rounded p times v.
+ * fp32; l accumulates fp32 p, acc accumulates bf16-rounded p times v
+ * (fp32_p != 0: acc accumulates fp32 p times v, the contract of the SIMT
+ * kernel attn_kv_kernel_x, attention_decode.cu:506-878).
  * Writes partials [16][NC][130] for every chunk with start <= limit; when
  * limit < C also writes out[qh*128+d] = bf16(acc/l) (the direct path). ---- */
-void orc_decode_chunks(const uint16_t* q, uint32_t limit, uint32_t layer,
-                       const uint16_t* pool, const uint32_t* pt, uint32_t P, uint32_t maxp,
-                       uint32_t C, uint32_t NC, float* partials, uint16_t* out) {
+void orc_decode_chunks_p(const uint16_t* q, uint32_t limit, uint32_t layer,
+                         const uint16_t* pool, const uint32_t* pt, uint32_t P, uint32_t maxp,
+                         uint32_t C, uint32_t NC, float* partials, uint16_t* out, int fp32_p) {
     const float scale = 0.08838834764831845f;
     for (uint32_t qh = 0; qh < HQ; ++qh) {
         const uint32_t kvh = qh / GROUP;
@@ -263,7 +265,10 @@ void orc_decode_chunks(const uint16_t* q, uint32_t limit, uint32_t layer,
                 for (uint32_t p = 0; p < 16u; ++p) {
                     const float pw = expf(sc[p] - mn);
                     ls += pw;
-                    qp[p] = orc_bf2f(orc_f2bf(pw));
+                    /* bf16-P (HMMA path) rounds P before P.V; fp32-P
+                     * (the SIMT fallback, attention_decode.cu:506-878) uses
+                     * it as is. */
+                    qp[p] = fp32_p ? pw : orc_bf2f(orc_f2bf(pw));
                 }
                 l = ls;
                 m = mn;
@@ -283,6 +288,12 @@ void orc_decode_chunks(const uint16_t* q, uint32_t limit, uint32_t layer,
                     out[qh * 128u + d] = orc_f2bf(l > 0.f ? acc[d] / l : 0.f);
         }
     }
+}
+
+void orc_decode_chunks(const uint16_t* q, uint32_t limit, uint32_t layer,
+                       const uint16_t* pool, const uint32_t* pt, uint32_t P, uint32_t maxp,
+                       uint32_t C, uint32_t NC, float* partials, uint16_t* out) {
+    orc_decode_chunks_p(q, limit, layer, pool, pt, P, maxp, C, NC, partials, out, 0);
 }
 
 /* ---- two-level merge in double (native/tests/kernel_ops.cpp:2011-2059

@@ -107,3 +107,16 @@ def test_prefill_debug_hooks(pkg, kvm):
     finally:
         kvm.debug_prefill_packing(was)
     assert was is True
+
+
+def test_prefill_status_hook_without_gpu(pkg, kvm):
+    """The prefill status read-back validates its argument and, with no GPU
+    in the process, reports a HIP error instead of crashing."""
+    assert kvm.lib().mc_kv_debug_prefill_status(None, 0) == 1
+    assert b"NULL" in kvm.lib().mc_last_error()
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present: the GPU prefill tests read the status")
+    with pytest.raises(pkg.McError) as e:
+        kvm.debug_prefill_status()
+    assert e.value.status == 3

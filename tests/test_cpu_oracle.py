@@ -246,6 +246,33 @@ def test_decode_chunk_partial_is_chunk_softmax(orc):
             assert np.linalg.norm(p[2:] - acc) / np.linalg.norm(acc) < 4e-3  # bf16 P
 
 
+def test_decode_chunk_fp32p_is_exact_chunk_softmax(orc):
+    """fp32-P partials are the chunk softmax statistics with P unrounded:
+    acc = sum exp(s - m) v to fp32 summation accuracy (1e-5), far tighter than
+    the bf16-P bound above; and they differ from the bf16-P partials (which
+    round P), so the flag is live."""
+    q, pool, pt, P, maxp = _rand_case(orc, 11, 300)
+    C, NC, limit = 64, 8, 299
+    parts, _ = orc.decode_chunks(q, limit, 0, pool, pt, P, maxp, C, NC, fp32_p=True)
+    parts_b, _ = orc.decode_chunks(q, limit, 0, pool, pt, P, maxp, C, NC)
+    qf = orc.bf16_to_f32(q[:2048]).reshape(16, 128).astype(np.float64)
+    for h in (0, 9, 15):
+        for c in (0, 4):
+            js = range(c * C, min(c * C + C, limit + 1))
+            K = np.stack([orc_kv(pool, P, maxp, 0, pt, j, 0, h // 8) for j in js])
+            V = np.stack([orc_kv(pool, P, maxp, 0, pt, j, 1, h // 8) for j in js])
+            s = K @ qf[h] / math.sqrt(128)
+            m = s.max()
+            w = np.exp(s - m)
+            p = parts[h, c].astype(np.float64)
+            assert abs(p[0] - m) < 1e-5
+            assert abs(p[1] - w.sum()) / w.sum() < 1e-5
+            acc = w @ V
+            assert np.linalg.norm(p[2:] - acc) / np.linalg.norm(acc) < 1e-5
+            pb = parts_b[h, c].astype(np.float64)
+            assert np.linalg.norm(pb[2:] - acc) / np.linalg.norm(acc) > 1e-5
+
+
 def test_merge2_vs_logsumexp(orc):
     """The two-level merge equals a direct numpy fold of all partials (order
     independent in exact arithmetic), with l == 0 partials ignored."""

@@ -22,6 +22,26 @@ pytestmark = pytest.mark.gpu
 POISON = 0xDCBA
 
 
+def n_records(NC, C):
+    """Records per query head of a decode launch: one per workgroup range of
+    ceil(NC / 256) chunks (C % 64 == 0), else one per chunk."""
+    cpw = -(-NC // 256) if (C % 64 == 0 and NC > 256) else 1
+    return -(-NC // cpw)
+
+
+class fp32p_mode:
+    """Temporarily sets the decode P.V precision (1 = fp32 P)."""
+
+    def __init__(self, kvm, fp32_p):
+        self.kvm, self.fp32_p = kvm, fp32_p
+
+    def __enter__(self):
+        self.prev = self.kvm.debug_decode_fp32p(self.fp32_p)
+
+    def __exit__(self, *a):
+        self.kvm.debug_decode_fp32p(self.prev)
+
+
 def make_case(orc, P, maxp, L, layer, pt, seq, seed, lo=-1.0, hi=1.0):
     lcg = Lcg(seed)
     pool = np.full(maxp * P * 512 * L, POISON, dtype=np.uint16)
@@ -261,10 +281,10 @@ def test_phase0_matches_rope_then_attend(kvm, orc, dev, limit):
     check_vs_ref(orc, from_dev(out_b), ref, f"phase0 limit={limit}")
 
 
-def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed, step=37):
+def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed, step=37, P=32):
     import torch
     rng = np.random.default_rng(seed)
-    P, L, layer = 32, 2, 1
+    L, layer = 2, 1
     pages_per = -(-(ctx + 1) // P)
     maxp = pages_per * B + 3  # shared pool, pages of all slots interleaved
     perm = rng.permutation(maxp).astype(np.uint32)
@@ -301,7 +321,8 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed, step=37):
     # single-session runs on a second copy of the pool
     d_pool1 = to_dev(pool, dev)
     singles = []
-    parts_b = from_dev(parts, np.float32).reshape(B, 16 * NC * 130)
+    nrec = 16 * n_records(NC, C) * 130  # a slot's records (the rest is unused)
+    parts_b = from_dev(parts, np.float32)[:B * nrec].reshape(B, nrec)
     parts2_b = from_dev(parts2, np.float32).reshape(B, 16 * 32 * 130)
     for s in range(B):
         p1 = torch.zeros(16 * NC * 130, dtype=torch.float32, device=dev)
@@ -313,7 +334,7 @@ def _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed, step=37):
         torch.cuda.synchronize()
         singles.append(from_dev(o1))
         # partials and level-2 partials too (bytes, so NaN payloads compare)
-        assert np.array_equal(from_dev(p1, np.uint32), parts_b[s].view(np.uint32)), s
+        assert np.array_equal(from_dev(p1, np.uint32)[:nrec], parts_b[s].view(np.uint32)), s
         assert np.array_equal(from_dev(p2, np.uint32), parts2_b[s].view(np.uint32)), s
     assert np.array_equal(got, np.stack(singles)), "batched != single (bitwise)"
     assert np.array_equal(pool_b, from_dev(d_pool1))
@@ -336,8 +357,18 @@ def test_batch_vs_single_ctx600(kvm, orc, dev, B, C, ph0):
     _batch_case(kvm, orc, dev, B, C, 600, ph0, seed=B * 100 + C + ph0)
 
 
-def test_batch_vs_single_8x2048(kvm, orc, dev):
-    _batch_case(kvm, orc, dev, 8, 64, 2047, True, seed=8)
+@pytest.mark.parametrize("P", [32, 64])
+def test_batch_vs_single_8x2048(kvm, orc, dev, P):
+    """Config C3's shape (8 sessions x 2048 context, 64-position chunks) at
+    both page sizes, P = 64 being the benchmark's."""
+    _batch_case(kvm, orc, dev, 8, 64, 2047, True, seed=8 + P, P=P)
+
+
+@pytest.mark.parametrize("B,C,ctx", [(4, 64, 600), (3, 256, 9000), (2, 128, 20000)])
+def test_batch_vs_single_page64(kvm, orc, dev, B, C, ctx):
+    """64-token pages (one page id per 16-position tile, several tiles per
+    page) through the batched and single-session kernels."""
+    _batch_case(kvm, orc, dev, B, C, ctx, True, seed=B + C, P=64)
 
 
 @pytest.mark.parametrize("C,ph0", [(64, True), (256, False)])
@@ -469,3 +500,86 @@ def test_batch_random_cases(kvm, orc, dev, B, C, ctx, ph0, step, seed):
     calls and within tolerance of the oracle."""
     print(f"B={B} C={C} ctx={ctx} ph0={ph0} step={step} seed={seed}", flush=True)
     _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed=seed, step=step)
+
+
+def test_reuse_buffers_new_data(kvm, orc, dev):
+    """Back-to-back launches on the same scratch buffers with different
+    queries and limits: each output matches a fresh computation (no stale
+    record of an earlier call is ever folded)."""
+    import torch
+    rng = np.random.default_rng(77)
+    P, L, layer, C = 64, 1, 0, 256
+    ctx = 40000
+    maxp = -(-ctx // P) + 1
+    pt = rng.permutation(maxp).astype(np.uint32)
+    lay = kvm.KvLayout(maxp, P, L)
+    pool = randn_bf16(rng, lay.total_elems(), 0.4)
+    d_pool, d_pt = to_dev(pool, dev), to_dev(pt, dev)
+    NC = -(-ctx // C)
+    parts = torch.zeros(16 * NC * 130, dtype=torch.float32, device=dev)
+    parts2 = torch.zeros(16 * 32 * 130, dtype=torch.float32, device=dev)
+    out = torch.zeros(2048, dtype=torch.int16, device=dev)
+    for it, limit in enumerate([ctx - 1, 300, 17000, 5, ctx - 2, 256 * 40]):
+        q = randn_bf16(rng, 2560, 1.0)
+        d_q = to_dev(q, dev)
+        d_pos = to_dev(np.array([limit], dtype=np.uint32), dev)
+        for _ in range(3):
+            kvm.launch_attention_decode(d_q, d_pos, layer, d_pt, d_pool, lay, parts, NC, out,
+                                        chunk_pos=C, d_partials2=parts2)
+        torch.cuda.synchronize()
+        ref = orc.attn_ref(q.reshape(1, 2560), 1, limit, layer, pool, pt, P, maxp)[0]
+        check_vs_ref(orc, from_dev(out), ref, f"reuse it={it} limit={limit}")
+
+
+@pytest.mark.parametrize("C,limit,P", [(64, 599, 32), (64, 40, 64), (256, 3000, 64),
+                                       (48, 777, 8), (128, 2000, 4)])
+def test_fp32p_chunks_vs_oracle(kvm, orc, dev, C, limit, P):
+    """fp32-P mode (the reference's MC_ATTN_HMMA_OFF fallback): per-chunk
+    partials of the chunk kernel vs the fp32-P chunk oracle, which differs
+    from the GPU only in summation order (relL2 < 2e-5 after rescaling to the
+    oracle's m; the bf16-P partials differ from it by far more)."""
+    import torch
+    rng = np.random.default_rng(C + limit + P)
+    maxp = -(-(limit + 1) // P) + 2
+    pt = rng.permutation(maxp).astype(np.uint32)
+    L, layer = 2, 1
+    lay = kvm.KvLayout(maxp, P, L)
+    pool = randn_bf16(rng, lay.total_elems(), 0.5)
+    q = randn_bf16(rng, 2560, 1.0)
+    NC = -(-(limit + 1) // C) + 1
+    d_q, d_pool, d_pt = to_dev(q, dev), to_dev(pool, dev), to_dev(pt, dev)
+    d_pos = to_dev(np.array([limit], dtype=np.uint32), dev)
+    got = {}
+    for fp in (1, 0):
+        with fp32p_mode(kvm, fp):
+            parts = torch.full((16 * NC * 130,), float("nan"), dtype=torch.float32, device=dev)
+            out = torch.zeros(2048, dtype=torch.int16, device=dev)
+            kvm.launch_attention_decode_chunks(d_q, d_pos, layer, d_pt, d_pool, lay, parts, NC,
+                                               out, chunk_pos=C)
+            torch.cuda.synchronize()
+            got[fp] = (from_dev(parts, np.float32).reshape(16, NC, 130), from_dev(out))
+    rparts, rout = orc.decode_chunks(q, limit, layer, pool, pt, P, maxp, C, NC, fp32_p=True)
+    nv = limit // C + 1
+    if nv == 1:  # single chunk: the kernel writes the output, not partials
+        a = orc.bf16_to_f32(got[1][1]).astype(np.float64)
+        r = orc.bf16_to_f32(rout).astype(np.float64)
+        assert np.all(np.abs(a - r) <= orc.bf16_ulp(r) + 1e-30), np.abs(a - r).max()
+        return
+    rel = {}
+    for fp in (1, 0):
+        a, r = got[fp][0][:, :nv].astype(np.float64), rparts[:, :nv].astype(np.float64)
+        assert np.abs(a[..., 0] - r[..., 0]).max() < 1e-4
+        scale = np.exp(a[..., 0] - r[..., 0])[..., None]
+        rel[fp] = np.linalg.norm(a[..., 1:] * scale - r[..., 1:]) / np.linalg.norm(r[..., 1:])
+    assert rel[1] < 2e-5, rel
+    assert rel[0] > 4 * rel[1], rel
+
+
+@pytest.mark.parametrize("B,C,ctx,ph0", [(1, 64, 2048, True), (1, 256, 131072, True),
+                                         (4, 128, 9000, False), (8, 64, 2048, True),
+                                         (2, 48, 3000, True)])
+def test_fp32p_decode_vs_oracle(kvm, orc, dev, B, C, ctx, ph0):
+    """fp32-P decode outputs (single and batched) within the attention
+    tolerance of the double oracle, and batched == single."""
+    with fp32p_mode(kvm, 1):
+        _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed=ctx + B, P=64)

@@ -15,6 +15,15 @@ pytestmark = pytest.mark.gpu
 POISON = 0xDCBA
 
 
+@pytest.fixture(autouse=True)
+def barrier_status_clear(kvm, dev):
+    """Every prefill test must leave the per-half barrier timeout count at
+    zero (a timed-out wait may have produced wrong output silently)."""
+    kvm.debug_prefill_status(reset=True)
+    yield
+    assert kvm.debug_prefill_status(reset=True) == 0, "prefill half-barrier wait timed out"
+
+
 def run_prefill(kvm, orc, dev, T, base, S, P=32, seed=0, sentinel=False, check=True,
                 abs_check=True, kgrow=0.0, inputs=False):
     import torch
