@@ -395,37 +395,52 @@ def host_threads() -> int:
     return max(1, min(n, 16))
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_append_baseline(seconds: float):
-    """The oracle's kernel-exact RoPE append (oracle/kv_oracle.c
-    orc_rope_append, one thread) over one 8448-token chunk of one layer,
-    repeated for about `seconds`; same bytes as the GPU C2 line."""
+    """The CPU baseline's RoPE append (oracle/cpu_baseline.c cpb_rope_append,
+    -O3 -march=native, all host threads) over one 8448-token chunk of one
+    layer, repeated for about `seconds`; same bytes as the GPU C2 line."""
     import numpy as np
     import oracle
     T = 8448
     maxp = T // P
+    threads = host_threads()
     rng = np.random.default_rng(1)
     qkv0 = oracle.f32_to_bf16(rng.standard_normal(T * 2560, dtype=np.float32)).reshape(T, 2560)
     pt = rng.permutation(maxp).astype(np.uint32)
     pool = np.zeros(maxp * P * 512, dtype=np.uint16)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        qkv = qkv0.copy()
-        oracle.rope_append(qkv, T, 0, 0, pt, P, maxp, 1e4, 1, pool)
+    qkv = qkv0.copy()
+    _, how = oracle.cpu_baseline_lib(native=True)
+    oracle.cpb_rope_append(qkv, T, 0, 0, pt, P, maxp, 1e4, pool, threads, native=True)  # warm
+    n, dt = 0, 0.0
+    while dt < seconds:
+        np.copyto(qkv, qkv0)
+        t0 = time.perf_counter()
+        oracle.cpb_rope_append(qkv, T, 0, 0, pt, P, maxp, 1e4, pool, threads, native=True)
+        dt += time.perf_counter() - t0
         n += 1
-        dt = time.perf_counter() - t0
-        if dt >= seconds:
-            break
     per_chunk = dt / n
     all_bytes = T * 2560 * 2 * 2  # row read + q / K / V written
     return {"tokens_per_s": T / per_chunk, "gbs": all_bytes / per_chunk / 1e9,
-            "cores": 1, "kind": "port",
-            "sample": f"{n} x 8448-token append of one layer, {per_chunk * 1e3:.1f} ms each"}
+            "cores": threads, "kind": "port", "build": how, "cpu": cpu_model(),
+            "nproc": os.cpu_count(),
+            "sample": f"{n} x 8448-token append of one layer, {per_chunk * 1e3:.2f} ms each"}
 
 
 def cpu_baseline(seconds: float):
-    """The oracle's fp32 decode (oracle/kv_oracle.c orc_decode_cpu_mt) on host
-    cores: one layer of the C4 workload (131072 tokens) per call, repeated for
-    about `seconds`."""
+    """The CPU baseline's fp32 decode (oracle/cpu_baseline.c cpb_decode: K/V
+    rows shared by the 8 query heads of a group, position segments on all
+    host threads, -O3 -march=native for this host): one layer of the C4
+    workload (131072 tokens) per call, repeated for about `seconds`."""
     import numpy as np
     import oracle
     ctx = 131072
@@ -436,10 +451,11 @@ def cpu_baseline(seconds: float):
                               / np.float32(128 ** 0.5))
     pt = rng.permutation(maxp).astype(np.uint32)
     q = oracle.f32_to_bf16(rng.standard_normal(2560, dtype=np.float32) / np.float32(11.3))
-    oracle.decode_cpu_mt(q, [ctx - 1], [pt], pool, 0, P, maxp, threads)  # warm
+    _, how = oracle.cpu_baseline_lib(native=True)
+    oracle.cpb_decode(q, [ctx - 1], [pt], pool, 0, P, maxp, threads, native=True)  # warm
     n, t0 = 0, time.perf_counter()
     while True:
-        oracle.decode_cpu_mt(q, [ctx - 1], [pt], pool, 0, P, maxp, threads)
+        oracle.cpb_decode(q, [ctx - 1], [pt], pool, 0, P, maxp, threads, native=True)
         n += 1
         dt = time.perf_counter() - t0
         if dt >= seconds:
@@ -450,6 +466,9 @@ def cpu_baseline(seconds: float):
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
+        "build": how,
+        "cpu": cpu_model(),
+        "nproc": os.cpu_count(),
         "sample": f"{n} single-layer decode steps at 131072 ctx (C4), fp32, "
                   f"{per_layer * 1e3:.2f} ms/layer",
         "us_per_layer": per_layer * 1e6,

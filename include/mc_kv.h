@@ -70,7 +70,9 @@ uint32_t mc_kv_prefill_split_kv(uint32_t tokens);
 /* ---- per-session page allocator (PagedKvAllocator, kv_cache.cpp:8-91) ---- */
 typedef struct mc_kv_allocator mc_kv_allocator_t;
 
-/* PagedKvAllocator::init: d_table is a device u32[max_pages]. */
+/* PagedKvAllocator::init: d_table is a device u32[max_pages], or NULL for a
+ * host-only allocator (same page choices and pages_synced accounting, no
+ * copies; used to plan or test tables without a device). */
 mc_status_t mc_kv_allocator_create(uint32_t* d_table, uint32_t max_pages,
                                    uint32_t tokens_per_page,
                                    mc_kv_allocator_t** out);

@@ -258,10 +258,11 @@ template <bool BATCH>
 __global__ void __launch_bounds__(256) merge_r_kernel(
     const float* __restrict__ rec, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NR, uint32_t C_rng,
-    uint16_t* __restrict__ out) {
+    uint32_t pos_max, uint16_t* __restrict__ out) {
     __shared__ float s_red[4 + 4 * 8 * 5];
     const uint32_t slot = blockIdx.y;
-    const uint32_t nr = n_valid_chunks(BATCH ? *slot_pos[slot] : *d_pos, C_rng, NR);
+    const uint32_t limit = min(BATCH ? *slot_pos[slot] : *d_pos, pos_max);  // as the chunk kernel
+    const uint32_t nr = n_valid_chunks(limit, C_rng, NR);
     if (nr <= 1u) return;  // the decode kernel wrote the output directly
     merge_task(rec + (size_t)slot * kHq * NR * kPartial, NR, nr, blockIdx.x,
                out + (size_t)slot * kHq * kD, threadIdx.x, s_red);
@@ -315,7 +316,8 @@ mc_status_t run_decode(ChunkLaunch L, float* partials2) {
     // Records of a range count as chunks of chunk_pos * cpw positions.
     if (nr_max <= kMaxRanges) {
         hipLaunchKernelGGL((merge_r_kernel<BATCH>), dim3(kMergeTasks, L.B), dim3(256), 0, L.st,
-                           L.partials, L.d_pos, L.slot_pos, nr_max, L.C * L.cpw, L.out);
+                           L.partials, L.d_pos, L.slot_pos, nr_max, L.C * L.cpw,
+                           pool_pos_max(L.ly), L.out);
         return check_launch("decode attention merge launch failed");
     }
     return launch_merge<BATCH>(L.partials, L.d_pos, L.slot_pos, L.B, nr_max, L.C * L.cpw,

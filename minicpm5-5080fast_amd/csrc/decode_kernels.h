@@ -227,6 +227,9 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // Page ids of the block's position range, staged once into LDS (read by
     // all tiles with a short LDS latency instead of a scalar-cache miss in
     // front of every tile's loads).
+    // Page ids are clamped to the pool (a corrupt table entry reads a wrong
+    // page instead of faulting the GPU).
+    const uint32_t page_max = ly.max_pages - 1u;
     const uint32_t page0 = (c_first * C) >> ly.log2p;
     const uint32_t npages_rng = ((min(c_end * C, limit + 1u) - 1u) >> ly.log2p) - page0 + 1u;
     const bool cached_pages = PAGE16 && npages_rng <= kPageCache;
@@ -245,12 +248,13 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             if (PAGE16 && cached_pages && !from_table)
                 page_u = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
             else if constexpr (PAGE16)
-                page_u = ((const __attribute__((address_space(4))) uint32_t*)(pt))
-                    [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)];
+                page_u = min(((const __attribute__((address_space(4))) uint32_t*)(pt))
+                                 [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)],
+                             page_max);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t p = min(t0 + grp + 4u * r, cend);
-                const uint32_t page = PAGE16 ? page_u : pt[p >> ly.log2p];
+                const uint32_t page = PAGE16 ? page_u : min(pt[p >> ly.log2p], page_max);
                 const uint16_t* src =
                     pool + token_base(ly, layer, page, p & ly.pmask) + kvh * kD + 8u * tok;
                 T.k[r] = ld16(src);
@@ -263,10 +267,11 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         if (PAGE16 && cached_pages && !from_table)
             page = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
         else if constexpr (PAGE16)
-            page = ((const __attribute__((address_space(4))) uint32_t*)(pt))
-                [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)];
+            page = min(((const __attribute__((address_space(4))) uint32_t*)(pt))
+                           [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)],
+                       page_max);
         else
-            page = pt[p >> ly.log2p];
+            page = min(pt[p >> ly.log2p], page_max);
         const uint16_t* src = pool + token_base(ly, layer, page, p & ly.pmask) + kvcol;
         if constexpr (VROWS) {  // K in operand layout, V as row loads
             const uint32_t cend = chunk_end(c);
@@ -275,7 +280,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t pr = min(t0 + grp + 4u * r, cend);
-                const uint32_t pg = PAGE16 ? page : pt[pr >> ly.log2p];
+                const uint32_t pg = PAGE16 ? page : min(pt[pr >> ly.log2p], page_max);
                 T.v[r] = ld16(pool + token_base(ly, layer, pg, pr & ly.pmask) + 256u +
                               kvh * kD + 8u * tok);
             }
@@ -384,7 +389,8 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     uint32_t fresh_v = 0u;
     uint2 fresh_kv = make_uint2(0u, 0u);
     const uint32_t limit_page =
-        owner ? ((const __attribute__((address_space(4))) uint32_t*)(pt))[limit >> ly.log2p]
+        owner ? min(((const __attribute__((address_space(4))) uint32_t*)(pt))[limit >> ly.log2p],
+                    page_max)
               : 0u;
     if (PH0) {  // every block reads the new token's k/v (a few cached bytes)
         invf = inv_freq[t64];
@@ -398,7 +404,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         fresh_kv = *reinterpret_cast<const uint2*>(src + 256u * (t64 >> 5) + (t64 & 31u) * 4u);
     }
     uint32_t staged_page = 0u;
-    if (cached_pages) staged_page = pt[page0 + min(tid, npages_rng - 1u)];
+    if (cached_pages) staged_page = min(pt[page0 + min(tid, npages_rng - 1u)], page_max);
 
     constexpr uint32_t RING = kRing;
     Tile R[RING];
@@ -732,6 +738,12 @@ __device__ __forceinline__ void merge_task(const float* __restrict__ rec, uint32
     __syncthreads();  // s_red is reused by the next task
 }
 
+// Last position the pool can hold (max_pages * P - 1, saturated to 32 bits).
+__host__ __device__ __forceinline__ uint32_t pool_pos_max(const DevLayout& ly) {
+    const uint64_t cap = (uint64_t)ly.max_pages << ly.log2p;
+    return cap > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)(cap - 1u);
+}
+
 __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
                                                    uint32_t NC) {
     const uint32_t n = limit / C + 1u;
@@ -752,6 +764,9 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
     uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
     float* __restrict__ partials, uint32_t NC, uint32_t rec_stride, uint16_t* __restrict__ out,
     const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw) {
+    // Positions beyond the pool's capacity do not exist: a limit past it is
+    // clamped, so page-table reads stay within its max_pages entries.
+    const uint32_t pos_max = pool_pos_max(ly);
     uint32_t slot = blockIdx.z, group = blockIdx.x, limit;
     if constexpr (BATCH) {
         // Work compaction: the (x, slot) workgroups are numbered densely over
@@ -773,7 +788,7 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
             const uint32_t lane = threadIdx.x & 63u;
             uint32_t lim = 0u, cnt = 0u;
             if (lane < B) {
-                lim = *slot_pos[lane];
+                lim = min(*slot_pos[lane], pos_max);
                 cnt = groups(n_valid_chunks(lim, Cc, NC));
             }
             // inclusive scan over the 64 lanes: row_shr 1, 2, 4, 8 within each
@@ -796,7 +811,7 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
         }
         if (slot >= B) return;  // past the last existing chunk group (uniform)
     } else {
-        limit = *d_pos;
+        limit = min(*d_pos, pos_max);
     }
     DecodeArgs a;
     a.q_row = q_rows + (size_t)slot * kRow;

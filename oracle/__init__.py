@@ -6,7 +6,9 @@ leg only; the product library (libminicpm_native.so) never calls it.
 
 The numeric functions live in kv_oracle.c (liboracle_kv.so, built by
 `make -C oracle`); each cites the reference file:line it restates. The page
-allocator model below is pure Python integer logic.
+allocator model below is pure Python integer logic. cpu_baseline.c is the
+speed-oriented CPU restatement bench.py times as its reported CPU baseline
+(checked against the oracle in tests/test_cpu_oracle.py).
 """
 from __future__ import annotations
 
@@ -52,6 +54,67 @@ def lib():
         L.orc_decode_cpu_mt.argtypes = [P, P, P, P, u32, u32, u32, u32, P, i32]
         _LIB = L
     return _LIB
+
+
+_CPB = {}
+
+
+def cpu_baseline_lib(native: bool = False):
+    """The CPU baseline library: the portable build (make -C oracle), or,
+    with native=True, a -O3 -march=native build for this host compiled into a
+    temporary directory (falls back to the portable build if gcc fails).
+    Returns (ctypes library, description of the build)."""
+    import subprocess
+    import tempfile
+    key = "native" if native else "portable"
+    if key in _CPB:
+        return _CPB[key]
+    path, how = os.path.join(_HERE, "libcpu_baseline.so"), "gcc -O3 -march=x86-64-v2"
+    if native:
+        d = tempfile.mkdtemp(prefix="cpb_")
+        cand = os.path.join(d, "libcpu_baseline_native.so")
+        r = subprocess.run(["gcc", "-O3", "-march=native", "-fPIC", "-std=c11", "-shared",
+                            os.path.join(_HERE, "cpu_baseline.c"), "-o", cand, "-lm",
+                            "-lpthread"], capture_output=True)
+        if r.returncode == 0:
+            path, how = cand, "gcc -O3 -march=native"
+    if not os.path.exists(path):
+        subprocess.run(["make", "-s", "-C", _HERE, "libcpu_baseline.so"], check=True)
+    L = C.CDLL(path)
+    P, u32 = C.c_void_p, C.c_uint32
+    L.cpb_decode_state_bytes.restype = C.c_size_t
+    L.cpb_decode_state_bytes.argtypes = [u32, u32]
+    L.cpb_decode.argtypes = [P, P, P, P, u32, u32, u32, u32, u32, P, P, C.c_int]
+    L.cpb_rope_append.argtypes = [P, u32, u32, u32, P, u32, u32, P, P, C.c_int]
+    _CPB[key] = (L, how)
+    return _CPB[key]
+
+
+def cpb_decode(q_rows, limits, page_tables, pool, layer, P, maxp, threads, nseg=None,
+               native=False):
+    """Speed-oriented fp32 CPU decode of B sessions (cpu_baseline.c)."""
+    L, _ = cpu_baseline_lib(native)
+    B = len(limits)
+    if nseg is None:
+        nseg = max(1, (4 * threads + 2 * B - 1) // (2 * B))
+    lim = np.ascontiguousarray(limits, dtype=np.uint32)
+    tabs = [np.ascontiguousarray(t, dtype=np.uint32) for t in page_tables]
+    ptrs = (C.c_void_p * B)(*[t.ctypes.data for t in tabs])
+    states = np.zeros(L.cpb_decode_state_bytes(B, nseg), dtype=np.uint8)
+    out = np.zeros((B, 2048), dtype=np.uint16)
+    L.cpb_decode(_p(np.ascontiguousarray(q_rows)), _p(lim), ptrs, _p(pool), layer, P, maxp, B,
+                 nseg, _p(states), _p(out), threads)
+    return out
+
+
+def cpb_rope_append(qkv, tokens, base_pos, layer, pt, P, maxp, theta, pool, threads,
+                    native=False):
+    """Speed-oriented RoPE + append (cpu_baseline.c); q rotated in place."""
+    L, _ = cpu_baseline_lib(native)
+    inv = inv_freq(theta)
+    pt = np.ascontiguousarray(pt, dtype=np.uint32)
+    L.cpb_rope_append(_p(qkv), tokens, base_pos, layer, _p(pt), P, maxp, _p(inv), _p(pool),
+                      threads)
 
 
 def _p(a: np.ndarray):

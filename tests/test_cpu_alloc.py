@@ -100,3 +100,42 @@ def test_allocator_model_closed_form(orc):
     assert m.ensure_pages_for(321) == "OOM"
     m.release_all()
     assert m.ensure_pages_for(64) == "OK" and m.shadow == [0, 1]
+
+
+def test_allocator_lazy_upload_matches_model(kvm, orc):
+    """The product allocator's lazy H2D rule (kv_cache.cpp:47-83): the table
+    prefix is re-uploaded only when pages were added, release_all resets the
+    synced count. Host-only allocator (no device table): pages_synced and the
+    shadow table are compared with the model after every grow / no-grow /
+    reset step; the model counts one upload per increase of its synced
+    prefix, so equal synced counts at every step mean equal uploads."""
+    rng = np.random.default_rng(3)
+    P, maxp = 32, 40
+    a = kvm.PagedKvAllocator(None, maxp, P)
+    m = orc.PagedKvAllocatorModel(maxp, P)
+    total, uploads_seen, prev_synced = 0, 0, 0
+    for step in range(300):
+        r = rng.random()
+        if r < 0.1:
+            a.release_all()
+            m.release_all()
+            total, prev_synced = 0, 0
+        else:
+            total = total + int(rng.integers(0, 70)) if r < 0.8 else total  # no-grow steps too
+            want = m.ensure_pages_for(total)
+            if want == "OOM":
+                with pytest.raises(kvm.McError) as e:
+                    a.ensure_pages_for(total, stream=0)
+                assert e.value.status == 5
+                a.release_all()
+                m.release_all()
+                total, prev_synced = 0, 0
+                continue
+            a.ensure_pages_for(total, stream=0)
+        assert a.pages_owned() == len(m.shadow)
+        assert a.pages_synced() == m.synced
+        assert a.host_table() == m.shadow
+        if a.pages_synced() > prev_synced:
+            uploads_seen += 1
+        prev_synced = a.pages_synced()
+    assert uploads_seen == m.uploads and uploads_seen > 10

@@ -300,3 +300,58 @@ def test_cpu_baseline_decode_matches_exact(orc):
     ref = orc.attn_ref(q.reshape(1, 2560), 1, 699, 0, pool, pt, P, maxp)[0]
     st = orc.compare_bf16(out, ref)
     assert st["rel_l2"] < 1e-2 and st["max_abs"] < 2e-2, st
+
+
+@pytest.mark.parametrize("native", [False, True])
+def test_fast_cpu_baseline_decode_matches_exact(orc, native):
+    """The speed-oriented CPU baseline (cpu_baseline.c: blocked online softmax,
+    K/V rows shared by the 8 query heads of a group, position segments merged
+    at the end) is within the attention tolerance of the double oracle, for 3
+    sessions with ragged limits, portable and -march=native builds."""
+    rng = np.random.default_rng(31)
+    P, maxp = 32, 3 * 40
+    pool = randn_bf16(rng, maxp * P * 512, 0.5)
+    perm = rng.permutation(maxp).astype(np.uint32)
+    pts = [perm[s::3].copy() for s in range(3)]
+    limits = [1200, 37, 0]
+    q = randn_bf16(rng, 3 * 2560, 1.0).reshape(3, 2560)
+    out = orc.cpb_decode(q, limits, pts, pool, 0, P, maxp, threads=5, native=native)
+    for s in range(3):
+        ref = orc.attn_ref(q[s].reshape(1, 2560), 1, limits[s], 0, pool, pts[s], P, maxp)[0]
+        st = orc.compare_bf16(out[s], ref)
+        assert st["rel_l2"] < 1e-2 and st["cos"] > 0.9999, (s, st)
+        assert st["max_abs"] < 2e-2 and st["mean_abs"] < 2e-3, (s, st)
+
+
+def test_fast_cpu_baseline_append_matches_reference(orc):
+    """The CPU baseline's RoPE append is within the reference's rope tolerance
+    (2 bf16 ulp + 1e-4, plus the fp32 angle's half-ulp error times the input
+    magnitude, as for the GPU kernel) of the double-precision rope_ref
+    statement on q and K, and copies V exactly."""
+    rng = np.random.default_rng(32)
+    T, base, P, theta = 300, 1000, 16, 1e4
+    maxp = -(-(base + T) // P) + 1
+    pt = rng.permutation(maxp).astype(np.uint32)
+    qkv = randn_bf16(rng, T * 2560, 1.0).reshape(T, 2560)
+    pool_a = np.zeros(maxp * P * 512, dtype=np.uint16)
+    pool_r = pool_a.copy()
+    qa, qr = qkv.copy(), qkv.copy()
+    orc.cpb_rope_append(qa, T, base, 0, pt, P, maxp, theta, pool_a, threads=3)
+    orc.rope_append(qr, T, base, 0, pt, P, maxp, theta, 0, pool_r)
+    inv = orc.inv_freq(theta).astype(np.float64)
+    d = np.arange(128)
+    ang_err = 2.0 ** -23 * (base + np.arange(T, dtype=np.float64))[:, None] * inv[d % 64][None, :]
+    src = orc.bf16_to_f32(qkv[:, :2304]).astype(np.float64).reshape(T, 18, 128)
+    extra = (np.abs(src) + np.abs(src[:, :, d ^ 64])) * ang_err[:, None, :]
+    a, r = orc.bf16_to_f32(qa[:, :2048]), orc.bf16_to_f32(qr[:, :2048])
+    assert np.all(np.abs(a - r) <= 2 * orc.bf16_ulp(r) + 1e-4 + extra[:, :16].reshape(T, 2048))
+    for t in range(T):
+        pos = base + t
+        off = orc.kv_off(P, maxp, 0, int(pt[pos // P]), pos % P, 0, 0, 0)
+        ka, kr = orc.bf16_to_f32(pool_a[off:off + 256]), orc.bf16_to_f32(pool_r[off:off + 256])
+        tol = 2 * orc.bf16_ulp(kr) + 1e-4 + extra[t, 16:].reshape(256)
+        assert np.all(np.abs(ka - kr) <= tol), t
+    for t in (0, 150, T - 1):
+        pos = base + t
+        off = orc.kv_off(P, maxp, 0, int(pt[pos // P]), pos % P, 0, 0, 0)
+        assert np.array_equal(pool_a[off + 256:off + 512], qkv[t, 2304:2560])

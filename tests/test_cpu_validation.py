@@ -86,7 +86,8 @@ def test_prefill_and_rope_rejects(pkg, lib):
 
 def test_allocator_and_pool_rejects(pkg, lib):
     h = C.c_void_p()
-    assert lib.mc_kv_allocator_create(None, 8, 32, C.byref(h)) == INV
+    assert lib.mc_kv_allocator_create(None, 8, 32, C.byref(h)) == 0  # host-only allocator
+    lib.mc_kv_allocator_destroy(h)
     assert lib.mc_kv_allocator_create(FAKE, 8, 48, C.byref(h)) == INV
     assert lib.mc_kv_allocator_create(FAKE, 0, 32, C.byref(h)) == INV
     assert lib.mc_kv_allocator_create(FAKE, 8, 32, None) == INV

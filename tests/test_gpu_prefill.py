@@ -162,6 +162,29 @@ def test_prefill_packed_jobs(kvm, orc, dev):
         assert st["max_abs"] < 2e-2 and st["mean_abs"] < 2e-3, (t0, st)
 
 
+def test_prefill_bench_workload_base0(kvm, orc, dev):
+    """The benchmark's prefill workload: 8448 rows at base 0 (32-row
+    workgroups, greedy dispatch, causal tiles of very different weight).
+    Packed and greedy settings give bit-identical outputs (packing only
+    applies after a long prefix); row windows at the start, middle and end
+    are checked against the oracle."""
+    T, base, P = 8448, 0, 64
+    prev = kvm.debug_prefill_packing(True)
+    try:
+        packed, (q, pool, pt, maxp, layer) = run_prefill(kvm, orc, dev, T, base, 1, P=P,
+                                                         seed=4, check=False, inputs=True)
+        kvm.debug_prefill_packing(False)
+        greedy = run_prefill(kvm, orc, dev, T, base, 1, P=P, seed=4, check=False)
+    finally:
+        kvm.debug_prefill_packing(prev)
+    assert np.array_equal(packed, greedy)
+    for t0 in (0, 31, 4200, T - 8):
+        ref = orc.attn_ref(q[t0:t0 + 8], 8, base + t0, layer, pool, pt, P, maxp)
+        st = orc.compare_bf16(packed[t0:t0 + 8], ref)
+        assert st["rel_l2"] < 1e-2 and st["cos"] > 0.9999, (t0, st)
+        assert st["max_abs"] < 2e-2 and st["mean_abs"] < 2e-3, (t0, st)
+
+
 def _random_prefill_cases(n, seed):
     import random
     rnd = random.Random(seed)
