@@ -156,16 +156,14 @@ def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
                                             chunk_pos=C, d_partials2=parts2)
         return f
 
-    def chunks_on(pool):
-        def f():
-            for l in range(LAYERS):
-                kvm.launch_attention_decode_chunks(qs[l * 2560:], pos, l, pt, pool, lay,
-                                                   parts, NC, out[l * 2048:],
-                                                   d_inv_freq=inv, chunk_pos=C)
-        return f
-
     step = timer.capture([step_on(p) for p in pools])
-    chunks_only = timer.capture([chunks_on(p) for p in pools])
+    # The chunk kernel alone (production configuration, merge skipped): the
+    # switch is read when the launches are issued, i.e. while capturing.
+    prev = kvm.debug_decode_records_only(True)
+    try:
+        chunks_only = timer.capture([step_on(p) for p in pools])
+    finally:
+        kvm.debug_decode_records_only(prev)
     timer.run(step, warmup)
     ms = timer.run(step, steps)
     ms_med = timer.median(step)
@@ -182,6 +180,7 @@ def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
         "tokens_per_s": 1e3 / ms,
         "chunk_kernel_us": ms_chunk * 1e3 / LAYERS,
         "chunk_kernel_gbs": bytes_layer / (ms_chunk * 1e-3 / LAYERS) / 1e9,
+        "merge_kernel_us": (ms - ms_chunk) * 1e3 / LAYERS,
         "algorithmic_bytes_per_layer": bytes_layer,
         "pool_copies_rotated": rot,
     }
@@ -395,6 +394,17 @@ def host_threads() -> int:
     return max(1, min(n, 16))
 
 
+def decode_sources_sha16() -> str:
+    """Hash of the decode kernel sources (the PMC traffic file records the
+    hash it was measured with)."""
+    import hashlib
+    h = hashlib.sha256()
+    d = os.path.join(ROOT, "minicpm5-5080fast_amd", "csrc")
+    for f in ("decode_kernels.h", "decode_bf16p.hip", "attention_decode.hip", "kv_common.h"):
+        h.update(open(os.path.join(d, f), "rb").read())
+    return h.hexdigest()[:16]
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -600,14 +610,22 @@ def main():
     }
     if head:
         ach = head["chunk_kernel_gbs"]
-        traffic = None  # HBM bytes per launch measured with rocprofv3 PMC passes
+        # HBM bytes per launch from two rocprofv3 PMC passes (FETCH_SIZE,
+        # WRITE_SIZE), valid only for the kernel sources they were measured
+        # on: the file records a hash of those sources.
+        traffic, note = None, "no PMC measurement for these kernel sources"
         tf = os.path.join(ROOT, "profiles", "decode_chunk_c4_traffic.txt")
         if os.path.exists(tf):
-            traffic = json.load(open(tf)).get("traffic_bytes")
+            rec = json.load(open(tf))
+            if rec.get("sources_sha16") == decode_sources_sha16():
+                traffic, note = rec.get("traffic_bytes"), rec.get("source")
+            else:
+                note = "PMC file is stale (kernel sources changed since it was measured)"
         line["roofline"] = {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS,
                             "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                            "traffic": traffic,
-                            "kernel": "decode_chunk_kernel<true,false> (C4 layer)",
+                            "traffic": traffic, "traffic_note": note,
+                            "kernel": "decode_chunk_kernel<true,false,true,4,true,false> "
+                                      "(C4 layer, merge skipped)",
                             "kernel_us": round(head["chunk_kernel_us"], 3)}
     print(json.dumps(line), flush=True)
 

@@ -268,6 +268,13 @@ mc_status_t mc_kv_debug_prefill_status(uint32_t* barrier_timeouts, uint32_t rese
  * was captured with. */
 mc_status_t mc_kv_debug_decode_fp32p(uint32_t fp32_p, uint32_t* previous);
 
+/* Measurement switch (process-wide, default 0): with enable != 0,
+ * mc_kv_attention_decode and mc_kv_attention_decode_batch launch only the
+ * chunk kernel (records written, d_out not produced), so a benchmark can
+ * time that kernel alone in its production configuration. The previous
+ * value goes to *previous when not NULL. No reference counterpart. */
+mc_status_t mc_kv_debug_decode_records_only(uint32_t enable, uint32_t* previous);
+
 /* Library build identity, e.g. "minicpm-kv gfx950". */
 const char* mc_kv_build_info(void);
 

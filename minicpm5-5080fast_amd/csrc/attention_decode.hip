@@ -250,22 +250,111 @@ mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
 }
 
 
-// Stand-alone fold of decode records with the fused merge's arithmetic (same
-// tasks, same order), for launches that cannot merge inside the decode
-// kernel: outputs are bit-identical either way. grid = (64 tasks, B slots),
-// block = 256. C_rng = positions per record range, NR = record stride.
-template <bool BATCH>
+// Fold of the decode records {m, l, acc[128]} of one (slot, query head,
+// slice of 4Q dims) per 256-thread block: record lane rl = t / Q (of
+// 256 / Q lanes) holds records rl + k * lanes, k < RPT, dim quad q = t % Q
+// dims 4q..4q+3 of the slice. Every record slot of the buffer is loaded
+// before the limit arrives (they all lie in the caller's buffer; the ones
+// past the limit's record count are masked), so the fold costs one memory
+// round. M = max m over records with l != 0, f = exp(m - M); each lane sums
+// l f and acc f over its records in k order, then the lanes are combined by
+// a fixed tree (xor-shuffles within a wave, then waves 0..3 in order), so
+// the result is deterministic and the same for batched and single launches.
+// out = bf16(A / L). grid = (16 * 32 / Q slices, B slots).
+template <bool BATCH, uint32_t Q, uint32_t RPT>
 __global__ void __launch_bounds__(256) merge_r_kernel(
     const float* __restrict__ rec, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NR, uint32_t C_rng,
     uint32_t pos_max, uint16_t* __restrict__ out) {
-    __shared__ float s_red[4 + 4 * 8 * 5];
+    static_assert(Q == 1u || Q == 2u || Q == 4u || Q == 8u, "dim quads per block");
+    constexpr uint32_t kSlices = 32u / Q;  // blocks per head
+    constexpr uint32_t kLanes = 256u / Q;
+    __shared__ float s_mx[4];
+    __shared__ float s_sum[4][Q][5];
+    const uint32_t t = threadIdx.x, wave = t >> 6;
     const uint32_t slot = blockIdx.y;
+    const uint32_t head = blockIdx.x / kSlices;
+    const uint32_t q = t % Q, rl = t / Q;
+    const uint32_t d = (blockIdx.x % kSlices) * 4u * Q + 4u * q;
+    const float* hb = rec + ((size_t)slot * kHq + head) * NR * kPartial;
+    float2 ml[RPT], a01[RPT], a23[RPT];
+#pragma unroll
+    for (uint32_t k = 0; k < RPT; ++k) {
+        const float* base = hb + (size_t)min(rl + k * kLanes, NR - 1u) * kPartial;
+        ml[k] = *reinterpret_cast<const float2*>(base);
+        a01[k] = *reinterpret_cast<const float2*>(base + 2 + d);  // rows are 8-byte aligned
+        a23[k] = *reinterpret_cast<const float2*>(base + 4 + d);
+    }
     const uint32_t limit = min(BATCH ? *slot_pos[slot] : *d_pos, pos_max);  // as the chunk kernel
     const uint32_t nr = n_valid_chunks(limit, C_rng, NR);
-    if (nr <= 1u) return;  // the decode kernel wrote the output directly
-    merge_task(rec + (size_t)slot * kHq * NR * kPartial, NR, nr, blockIdx.x,
-               out + (size_t)slot * kHq * kD, threadIdx.x, s_red);
+    if (nr <= 1u) return;  // the chunk kernel wrote the output directly (uniform)
+    float mx = -INFINITY;
+#pragma unroll
+    for (uint32_t k = 0; k < RPT; ++k)
+        if (rl + k * kLanes < nr && ml[k].y != 0.f) mx = fmaxf(mx, ml[k].x);
+    mx = wave_max(mx);
+    if ((t & 63u) == 0u) s_mx[wave] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+    float L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t k = 0; k < RPT; ++k) {
+        if (rl + k * kLanes < nr && ml[k].y != 0.f) {
+            const float f = expf(ml[k].x - M);
+            L += ml[k].y * f;
+            A += f32x4{a01[k].x, a01[k].y, a23[k].x, a23[k].y} * f;
+        }
+    }
+#pragma unroll
+    for (uint32_t x = Q; x < 64u; x <<= 1) {
+        L += __shfl_xor(L, (int)x);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) A[k] += __shfl_xor(A[k], (int)x);
+    }
+    if ((t & 63u) < Q) {
+        s_sum[wave][q][0] = L;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s_sum[wave][q][1 + k] = A[k];
+    }
+    __syncthreads();
+    if (t < Q) {
+        float Lt = 0.f;
+        f32x4 At = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t w = 0; w < 4u; ++w) {
+            Lt += s_sum[w][t][0];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) At[k] += s_sum[w][t][1 + k];
+        }
+        uint16_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o[k] = f32_to_bf16(Lt > 0.f ? At[k] / Lt : 0.f);
+        *reinterpret_cast<uint2*>(out + ((size_t)slot * kHq + head) * kD + d) =
+            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
+                       (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+    }
+}
+
+// Block shape of the record merge: 8 dim quads (32 dims, whole 128-byte
+// lines of a record per lane) and 32 record lanes with RPT = ceil(NR / 32)
+// records each; 64 blocks per slot. Measured at C4 (256 records per head):
+// merge span 2.8 us against 3.4 / 3.0 / 4.2 us for 64 / 128 / 256 record
+// lanes per block (more blocks, fewer records per lane).
+template <bool BATCH>
+void launch_merge_r(const ChunkLaunch& L, uint32_t NR) {
+    const uint32_t Q = 8u, lanes = 32u;
+    const uint32_t rpt = (NR + lanes - 1u) / lanes;
+    const dim3 grid(kHq * 32u / Q, L.B);
+    const uint32_t C_rng = L.C * L.cpw, pmax = pool_pos_max(L.ly);
+#define MC_MERGE_R(QQ, RR)                                                                  \
+    hipLaunchKernelGGL((merge_r_kernel<BATCH, QQ, RR>), grid, dim3(256), 0, L.st, L.partials, \
+                       L.d_pos, L.slot_pos, NR, C_rng, pmax, L.out)
+    if (rpt <= 1u) MC_MERGE_R(8u, 1u);
+    else if (rpt <= 2u) MC_MERGE_R(8u, 2u);
+    else if (rpt <= 4u) MC_MERGE_R(8u, 4u);
+    else MC_MERGE_R(8u, 8u);
+#undef MC_MERGE_R
 }
 
 bool chunk_args_ok(uint32_t max_chunks, uint32_t chunk_pos) {
@@ -299,11 +388,15 @@ bool fp32p_on() {
     }
     return v != 0u;
 }
+// Measurement switch (debug hook): decode launches stop after the chunk
+// kernel, so its time can be taken alone in the production configuration.
+std::atomic<uint32_t> g_records_only{0u};
+
 // Runs one decode: the chunk kernel writes one record per (range, query
-// head), or the output when the context fits one range; merge_r_kernel
-// folds the records. Beyond kMaxRanges records per head (chunk sizes that
-// are not a multiple of 64 with more than 256 chunks) the reference's merges
-// fold them instead (two-level when partials2 is given).
+// head), or the output when the context fits one range; a merge kernel folds
+// the records: merge_p for at most 32 records per head, merge_r_kernel up to
+// kMaxRanges, beyond (chunk sizes that are not a multiple of 64 with more than
+// 256 chunks) the reference's two-level merge when partials2 is given.
 template <bool BATCH>
 mc_status_t run_decode(ChunkLaunch L, float* partials2) {
     L.batched = BATCH;
@@ -312,12 +405,13 @@ mc_status_t run_decode(ChunkLaunch L, float* partials2) {
     L.rec_stride = nr_max;
     const mc_status_t st =
         fp32p_on() ? launch_chunk_kernel<true>(L) : launch_chunk_kernel<false>(L);
-    if (st != MC_OK) return st;
+    if (st != MC_OK || g_records_only.load(std::memory_order_relaxed) != 0u) return st;
     // Records of a range count as chunks of chunk_pos * cpw positions.
-    if (nr_max <= kMaxRanges) {
-        hipLaunchKernelGGL((merge_r_kernel<BATCH>), dim3(kMergeTasks, L.B), dim3(256), 0, L.st,
-                           L.partials, L.d_pos, L.slot_pos, nr_max, L.C * L.cpw,
-                           pool_pos_max(L.ly), L.out);
+    // Up to 32 records per head the reference's one-level fold (merge_p, one
+    // 128-thread block per (slot, head), thread = dim) is the faster merge
+    // (C3: 13.5 against 14.4 us/layer with merge_r); beyond, merge_r.
+    if (nr_max > kSplit2 && nr_max <= kMaxRanges) {
+        launch_merge_r<BATCH>(L, nr_max);
         return check_launch("decode attention merge launch failed");
     }
     return launch_merge<BATCH>(L.partials, L.d_pos, L.slot_pos, L.B, nr_max, L.C * L.cpw,
@@ -414,6 +508,12 @@ extern "C" mc_status_t mc_kv_debug_decode_fp32p(uint32_t fp32_p, uint32_t* previ
         return MC_E_INVALID_ARGUMENT;
     }
     const uint32_t prev = g_fp32p.exchange(fp32_p);
+    if (previous != nullptr) *previous = prev;
+    return MC_OK;
+}
+
+extern "C" mc_status_t mc_kv_debug_decode_records_only(uint32_t enable, uint32_t* previous) {
+    const uint32_t prev = g_records_only.exchange(enable ? 1u : 0u);
     if (previous != nullptr) *previous = prev;
     return MC_OK;
 }

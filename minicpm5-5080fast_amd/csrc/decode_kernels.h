@@ -191,12 +191,6 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     auto& s_l = s_l_[half];
     auto& s_acc = s_acc_[half];
 
-    const uint32_t limit = a.limit;
-    const uint32_t nvalid = min(limit / C + 1u, NC);
-    const uint32_t c_first = group * cpw;
-    if (c_first >= nvalid) return;  // uniform over the block
-    const uint32_t c_end = min(c_first + cpw, nvalid);
-    const bool direct = nvalid <= cpw;  // the only range: write the output
     const uint32_t tid = threadIdx.x & 255u;
     // Wave index made provably wave-uniform so every tile / chunk decision
     // below compiles to scalar branches.
@@ -209,48 +203,27 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     const uint32_t* __restrict__ pt = a.pt;
     uint16_t* __restrict__ pool = a.pool;
     const uint32_t kvcol = kvh * kD + 8u * grp;  // within a token's K or V half
-
-    // Position `limit` is kept out of the streamed tiles and added as one extra
-    // tile from LDS by wave 0 of the owning block: with phase0 its K/V come
-    // from the qkv row, otherwise from the pool. Both modes therefore run the
-    // same arithmetic (phase0 output == append-then-attend output, bitwise) and
-    // the streaming loop never patches registers.
-    const uint32_t last_pos = limit - 1u;  // last streamed position
-    auto chunk_end = [&](uint32_t c) { return min(c * C + C - 1u, last_pos); };
-    auto chunk_tiles = [&](uint32_t c) {
-        const uint32_t cs = c * C;
-        return (limit == 0u || last_pos < cs) ? 0u : (chunk_end(c) - cs) / kTile + 1u;
-    };
+    // Page ids are clamped to the pool and table indices to the table's
+    // max_pages entries (a corrupt entry reads a wrong page instead of
+    // faulting the GPU).
+    const uint32_t page_max = ly.max_pages - 1u;
     // A 16-position tile starts 16-aligned, so with P >= 16 (PAGE16) it lies in
     // one page and the page id is wave-uniform: it is read through the scalar
     // path and does not serialize behind the vector loads in flight.
-    // Page ids of the block's position range, staged once into LDS (read by
-    // all tiles with a short LDS latency instead of a scalar-cache miss in
-    // front of every tile's loads).
-    // Page ids are clamped to the pool (a corrupt table entry reads a wrong
-    // page instead of faulting the GPU).
-    const uint32_t page_max = ly.max_pages - 1u;
-    const uint32_t page0 = (c_first * C) >> ly.log2p;
-    const uint32_t npages_rng = ((min(c_end * C, limit + 1u) - 1u) >> ly.log2p) - page0 + 1u;
-    const bool cached_pages = PAGE16 && npages_rng <= kPageCache;
-    // `direct` reads the page id from the table itself (scalar path for
-    // PAGE16) instead of the LDS copy; the first tiles use it so that they
-    // do not wait for the staging barrier.
-    auto load_tile = [&](Tile& T, uint32_t c, uint32_t j, bool from_table) {
-        const uint32_t t0 = c * C + j * kTile;
+    auto table_page = [&](uint32_t t0) {
+        return min(((const __attribute__((address_space(4))) uint32_t*)(pt))
+                       [__builtin_amdgcn_readfirstlane(min(t0 >> ly.log2p, page_max))],
+                   page_max);
+    };
+    // Loads the tile of rows t0..t0+15, rows past `cend` replaced by row
+    // `cend` (so no masked row reads memory past the context); page_u is the
+    // page of t0 (PAGE16).
+    auto load_rows = [&](Tile& T, uint32_t t0, uint32_t cend, uint32_t page_u) {
         if constexpr (ROWS) {
             // Row loads: lane (q = lane/16, x = lane%16) reads the 16-byte chunk x
             // of the K and V head rows of tokens t0 + q + 4r (r < 4), so every 16
             // lanes read one whole 256-byte head row (whole 128-byte lines per
             // request). xpose() restores the MFMA operand layout through LDS.
-            const uint32_t cend = chunk_end(c);
-            uint32_t page_u = 0;
-            if (PAGE16 && cached_pages && !from_table)
-                page_u = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
-            else if constexpr (PAGE16)
-                page_u = min(((const __attribute__((address_space(4))) uint32_t*)(pt))
-                                 [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)],
-                             page_max);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t p = min(t0 + grp + 4u * r, cend);
@@ -262,19 +235,10 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             }
             return;
         }
-        const uint32_t p = min(t0 + tok, chunk_end(c));
-        uint32_t page;
-        if (PAGE16 && cached_pages && !from_table)
-            page = s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)];
-        else if constexpr (PAGE16)
-            page = min(((const __attribute__((address_space(4))) uint32_t*)(pt))
-                           [__builtin_amdgcn_readfirstlane(t0 >> ly.log2p)],
-                       page_max);
-        else
-            page = min(pt[p >> ly.log2p], page_max);
+        const uint32_t p = min(t0 + tok, cend);
+        const uint32_t page = PAGE16 ? page_u : min(pt[p >> ly.log2p], page_max);
         const uint16_t* src = pool + token_base(ly, layer, page, p & ly.pmask) + kvcol;
         if constexpr (VROWS) {  // K in operand layout, V as row loads
-            const uint32_t cend = chunk_end(c);
 #pragma unroll
             for (int m = 0; m < 4; ++m) T.k[m] = ld16(src + 32u * m);
 #pragma unroll
@@ -291,6 +255,45 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                 T.v[m] = ld16(src + 256u + 32u * m);
             }
         }
+    };
+
+    constexpr uint32_t RING = kRing;
+    Tile R[RING];
+    const uint32_t c_first = group * cpw;
+    const uint32_t limit = a.limit;
+    const uint32_t nvalid = min(limit / C + 1u, NC);
+    if (c_first >= nvalid) return;  // uniform over the block
+    const uint32_t c_end = min(c_first + cpw, nvalid);
+    const bool direct = nvalid <= cpw;  // the only range: write the output
+
+    // Position `limit` is kept out of the streamed tiles and added as one extra
+    // tile from LDS by wave 0 of the owning block: with phase0 its K/V come
+    // from the qkv row, otherwise from the pool. Both modes therefore run the
+    // same arithmetic (phase0 output == append-then-attend output, bitwise) and
+    // the streaming loop never patches registers.
+    const uint32_t last_pos = limit - 1u;  // last streamed position
+    auto chunk_end = [&](uint32_t c) { return min(c * C + C - 1u, last_pos); };
+    auto chunk_tiles = [&](uint32_t c) {
+        const uint32_t cs = c * C;
+        return (limit == 0u || last_pos < cs) ? 0u : (chunk_end(c) - cs) / kTile + 1u;
+    };
+    // Page ids of the block's position range, staged once into LDS (read by
+    // all tiles with a short LDS latency instead of a scalar-cache miss in
+    // front of every tile's loads).
+    const uint32_t page0 = (c_first * C) >> ly.log2p;
+    const uint32_t npages_rng = ((min(c_end * C, limit + 1u) - 1u) >> ly.log2p) - page0 + 1u;
+    const bool cached_pages = PAGE16 && npages_rng <= kPageCache;
+    // `from_table` reads the page id from the table itself (scalar path for
+    // PAGE16) instead of the LDS copy; the first tiles use it so that they
+    // do not wait for the staging barrier.
+    auto load_tile = [&](Tile& T, uint32_t c, uint32_t j, bool from_table) {
+        const uint32_t t0 = c * C + j * kTile;
+        uint32_t page_u = 0u;
+        if constexpr (PAGE16)
+            page_u = (cached_pages && !from_table)
+                         ? s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)]
+                         : table_page(t0);
+        load_rows(T, t0, chunk_end(c), page_u);
     };
     // Row-loaded tile -> operand layout (lane (row, group) holds dims
     // [32m + 8*group, +8) of token row, m < 4) through this wave's LDS tile:
@@ -406,8 +409,6 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     uint32_t staged_page = 0u;
     if (cached_pages) staged_page = min(pt[page0 + min(tid, npages_rng - 1u)], page_max);
 
-    constexpr uint32_t RING = kRing;
-    Tile R[RING];
     Tile& A = R[0];
     Tile& B = R[RING > 1u ? 1u : 0u];
     uint32_t ac = c_first, aj = wave;
@@ -653,90 +654,9 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(Acc[2], Acc[3]);
 }
 
-// ---- merge of the decode records ----
-constexpr uint32_t kMergeTasks = 64;  // 16 heads x 4 dim slices of 32
-constexpr uint32_t kMaxRanges = 256;  // records per head merge_task folds
-
-// One merge task on 256 threads (t = thread index within them): thread
-// (record lane rl = t / 8, dim quad t % 8) folds records rl, rl + 32, ...
-// (ascending), then the 32 record lanes are combined by a fixed tree
-// (xor-shuffles 8, 16, 32 within a wave, then waves 0..3 in order).
-// out = bf16(A / L) with M = max m over records with l != 0,
-// f = exp(m - M), L = sum l f, A = sum acc f (the reference merge rule).
-__device__ __forceinline__ void merge_task(const float* __restrict__ rec, uint32_t stride,
-                                           uint32_t nr, uint32_t task, uint16_t* out,
-                                           uint32_t t, float* s_red /* [4 + 4*8*5] */) {
-    const uint32_t head = task >> 2;
-    const uint32_t d = (task & 3u) * 32u + (t & 7u) * 4u;
-    const uint32_t rl = t >> 3;
-    const uint32_t w = t >> 6;
-    const float* base = rec + (size_t)head * stride * kPartial;
-    constexpr uint32_t kPer = kMaxRanges / 32u;  // records per thread
-    float2 ml[kPer], a01[kPer], a23[kPer];
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) {
-        const uint32_t r = rl + 32u * i;
-        const float* p = base + (size_t)(r < nr ? r : 0u) * kPartial;
-        if (32u * i < nr) {  // uniform: some lane of the loop trip has a record
-            ml[i] = *reinterpret_cast<const float2*>(p);
-            a01[i] = *reinterpret_cast<const float2*>(p + 2 + d);
-            a23[i] = *reinterpret_cast<const float2*>(p + 4 + d);
-        } else {
-            ml[i] = make_float2(0.f, 0.f);
-            a01[i] = a23[i] = make_float2(0.f, 0.f);
-        }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i)
-        if (rl + 32u * i < nr && ml[i].y != 0.f) mx = fmaxf(mx, ml[i].x);
-    mx = wave_max(mx);
-    if ((t & 63u) == 0u) s_red[w] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    float L = 0.f;
-    f32x4 A = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) {
-        if (rl + 32u * i < nr && ml[i].y != 0.f) {
-            const float f = expf(ml[i].x - M);
-            L += ml[i].y * f;
-            A += f32x4{a01[i].x, a01[i].y, a23[i].x, a23[i].y} * f;
-        }
-    }
-#pragma unroll
-    for (int x = 8; x <= 32; x <<= 1) {
-        L += __shfl_xor(L, x);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) A[k] += __shfl_xor(A[k], x);
-    }
-    float* s_w = s_red + 4;  // [4 waves][8 quads][5]
-    if ((t & 63u) < 8u) {
-        float* q = s_w + (w * 8u + (t & 7u)) * 5u;
-        q[0] = L;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) q[1 + k] = A[k];
-    }
-    __syncthreads();
-    if (t < 8u) {
-        float Lt = 0.f;
-        f32x4 At = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (uint32_t ww = 0; ww < 4u; ++ww) {
-            const float* q = s_w + (ww * 8u + t) * 5u;
-            Lt += q[0];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) At[k] += q[1 + k];
-        }
-        uint16_t o[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = f32_to_bf16(Lt > 0.f ? At[k] / Lt : 0.f);
-        *reinterpret_cast<uint2*>(out + head * kD + d) =
-            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16),
-                       (uint32_t)o[2] | ((uint32_t)o[3] << 16));
-    }
-    __syncthreads();  // s_red is reused by the next task
-}
+// Records per head the record merge folds (chunks_per_range keeps ranges
+// at or below it).
+constexpr uint32_t kMaxRanges = 256;
 
 // Last position the pool can hold (max_pages * P - 1, saturated to 32 bits).
 __host__ __device__ __forceinline__ uint32_t pool_pos_max(const DevLayout& ly) {

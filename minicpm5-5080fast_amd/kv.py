@@ -186,6 +186,15 @@ def debug_decode_fp32p(fp32_p: int) -> int:
     return prev.value
 
 
+def debug_decode_records_only(enable: bool) -> bool:
+    """Measurement switch: decode launches run only the chunk kernel (no
+    merge, no output). Returns the previous setting. Debug hook."""
+    prev = C.c_uint32(0)
+    check(lib().mc_kv_debug_decode_records_only(1 if enable else 0, C.byref(prev)),
+          "debug_decode_records_only")
+    return bool(prev.value)
+
+
 def launch_decode_advance(d_seq, d_next_token, d_seq_len, stream=None) -> None:
     check(lib().mc_kv_decode_advance(_ptr(d_seq), _ptr(d_next_token), _ptr(d_seq_len),
                                      _stream(stream)), "launch_decode_advance")
