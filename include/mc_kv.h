@@ -235,6 +235,40 @@ mc_status_t mc_debug_session_info(mc_session_t session, uint32_t* seq_len,
 /* Copies the first n token ids of the device sequence (n <= seq_len). */
 mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n);
 
+/* Session arena bytes (one device allocation per session, sized at create;
+ * reference session.cpp:651-654) and the decode chunk tier chosen for the
+ * session's context (session.cpp:659-662). 0 for a NULL session. */
+size_t mc_debug_session_arena_bytes(mc_session_t session);
+uint32_t mc_debug_session_attn_chunk(mc_session_t session);
+
+/* Decode-step breakdown (reference session.cpp:686-723): when MC_BREAKDOWN
+ * is set at mc_session_create, every eager mc_decode_one records events at
+ * its segment boundaries (a step replayed as a HIP graph records none; the
+ * hooks then report -2). Raw segments, in order:
+ * per layer {synthetic qkv row, phase0 decode attention}, then the tail
+ * (token write + sequence advance). raw_segments returns their count (0 when
+ * off); bucket_count / bucket_name / bucket_of describe the aggregation
+ * (qkv, attention, tail); collect writes the last step's segment times (ms)
+ * into out_ms[0..n) with n == raw_segments and returns n; 0 = off,
+ * -1 = bad arguments, -2 = no complete step recorded yet, -3 = HIP error.
+ * Call after the step returned (it synchronizes its stream). */
+int mc_debug_breakdown_raw_segments(mc_session_t session);
+int mc_debug_breakdown_bucket_count(void);
+const char* mc_debug_breakdown_bucket_name(int i);
+int mc_debug_breakdown_bucket_of(int raw);
+int mc_debug_breakdown_collect(mc_session_t session, double* out_ms, int n);
+
+/* Batch-group statistics (reference batch_group.cpp:869-886): steps run,
+ * their summed wall time (us) and the current member count. */
+mc_status_t mc_debug_batch_group_stats(mc_batch_group_t group, uint64_t* steps,
+                                       uint64_t* decode_us, uint32_t* members);
+
+/* Last mc_batch_step's time per bucket (ms) when MC_BATCH_BREAKDOWN was set
+ * at mc_batch_group_create (reference batch_group.cpp:888-927; buckets as
+ * mc_debug_breakdown_bucket_name). n must equal the bucket count; returns it,
+ * 0 = off, -1 = bad arguments, -2 = no complete step, -3 = HIP error. */
+int mc_debug_batch_breakdown_collect(mc_batch_group_t group, double* out_ms, int n);
+
 /* Prefill workgroup shape: 0 = 32 query rows on 8 waves, 1 = 16 rows on 4
  * waves, 2 = 16 rows on two 4-wave halves taking alternate key steps,
  * 0xFFFFFFFF = chosen per launch (default). All compute the same softmax;

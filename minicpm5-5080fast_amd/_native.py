@@ -74,6 +74,9 @@ _SIGS = {
     "mc_kv_debug_prefill_packing": (C.c_int, [_u32, _P]),
     "mc_kv_debug_prefill_status": (C.c_int, [_P, _u32]),
     "mc_kv_debug_decode_fp32p": (C.c_int, [_u32, _P]),
+    "mc_debug_breakdown_bucket_count": (C.c_int, []),
+    "mc_debug_breakdown_bucket_name": (C.c_char_p, [C.c_int]),
+    "mc_debug_breakdown_bucket_of": (C.c_int, [C.c_int]),
     "mc_kv_debug_decode_records_only": (C.c_int, [_u32, _P]),
 }
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include "error.h"
+#include "trace.h"
 #include "kv_common.h"
 
 namespace mckv {
@@ -33,6 +34,7 @@ __global__ void batch_advance_kernel(int32_t* const* __restrict__ slot_seq,
 
 extern "C" mc_status_t mc_kv_decode_advance(int32_t* d_seq, const int32_t* d_next_token,
                                             uint32_t* d_seq_len, void* stream) {
+    mckv::TraceRange trace_range("mc_kv_decode_advance");
     if (d_seq == nullptr || d_next_token == nullptr || d_seq_len == nullptr) {
         mckv::set_error("mc_kv_decode_advance: NULL argument");
         return MC_E_INVALID_ARGUMENT;
@@ -46,6 +48,7 @@ extern "C" mc_status_t mc_kv_batch_advance(int32_t* const* d_slot_seq,
                                            const int32_t* const* d_slot_tok,
                                            uint32_t* const* d_slot_pos, uint32_t n,
                                            void* stream) {
+    mckv::TraceRange trace_range("mc_kv_batch_advance");
     if (d_slot_seq == nullptr || d_slot_tok == nullptr || d_slot_pos == nullptr ||
         n == 0) {
         mckv::set_error("mc_kv_batch_advance: invalid args (n=%u)", n);

@@ -20,6 +20,7 @@
 
 #include "decode_kernels.h"
 #include "error.h"
+#include "trace.h"
 #include "kv_common.h"
 #include "kv_internal.h"
 
@@ -428,6 +429,7 @@ extern "C" mc_status_t mc_kv_attention_decode_chunks(
     const uint32_t* d_page_table, uint16_t* d_kv_pool, mc_kv_layout_t layout,
     float* d_partials, uint32_t max_chunks, uint16_t* d_out, void* stream,
     const float* d_inv_freq, uint32_t chunk_pos) {
+    mckv::TraceRange trace_range("mc_kv_attention_decode_chunks");
     DevLayout ly;
     if (d_q_rows == nullptr || d_pos == nullptr || d_page_table == nullptr ||
         d_kv_pool == nullptr || d_partials == nullptr || d_out == nullptr ||
@@ -451,6 +453,7 @@ extern "C" mc_status_t mc_kv_attention_decode(
     const uint32_t* d_page_table, uint16_t* d_kv_pool, mc_kv_layout_t layout,
     float* d_partials, uint32_t max_chunks, uint16_t* d_out, void* stream,
     const float* d_inv_freq, uint32_t chunk_pos, float* d_partials2) {
+    mckv::TraceRange trace_range("mc_kv_attention_decode");
     DevLayout ly;
     if (d_q_rows == nullptr || d_pos == nullptr || d_page_table == nullptr ||
         d_kv_pool == nullptr || d_partials == nullptr || d_out == nullptr ||
@@ -470,6 +473,7 @@ extern "C" mc_status_t mc_kv_attention_decode(
 extern "C" mc_status_t mc_kv_attention_decode_merge(
     const float* d_partials, const uint32_t* d_pos, uint32_t max_chunks,
     uint32_t chunk_pos, float* d_partials2, uint16_t* d_out, void* stream) {
+    mckv::TraceRange trace_range("mc_kv_attention_decode_merge");
     if (d_partials == nullptr || d_pos == nullptr || d_out == nullptr ||
         !chunk_args_ok(max_chunks, chunk_pos)) {
         set_error("mc_kv_attention_decode_merge: invalid args (max_chunks=%u "
@@ -486,6 +490,7 @@ extern "C" mc_status_t mc_kv_attention_decode_batch(
     uint32_t layer, const uint32_t* const* d_slot_pt, uint16_t* const* d_slot_kv,
     mc_kv_layout_t layout, float* d_partials, uint32_t max_chunks, uint16_t* d_out,
     void* stream, const float* d_inv_freq, uint32_t chunk_pos, float* d_partials2) {
+    mckv::TraceRange trace_range("mc_kv_attention_decode_batch");
     DevLayout ly;
     if (d_q_rows == nullptr || d_slot_pos == nullptr || d_slot_pt == nullptr ||
         d_slot_kv == nullptr || d_partials == nullptr || d_out == nullptr || B == 0 ||

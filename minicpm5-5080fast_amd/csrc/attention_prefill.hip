@@ -48,6 +48,7 @@
 #include <cmath>
 
 #include "error.h"
+#include "trace.h"
 #include "kv_common.h"
 #include "kv_internal.h"
 
@@ -684,6 +685,7 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
                                                mc_kv_layout_t layout, uint16_t* d_out,
                                                float* d_partials, uint32_t S_kv,
                                                void* stream) {
+    mckv::TraceRange trace_range("mc_kv_attention_prefill");
     DevLayout ly;
     if (d_q_rows == nullptr || d_base_pos == nullptr || d_page_table == nullptr ||
         d_kv_pool == nullptr || d_out == nullptr || tokens == 0 || S_kv == 0u ||

@@ -3,6 +3,9 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+
+#include "trace.h"
 
 namespace mckv {
 
@@ -22,6 +25,11 @@ mc_status_t check_hip(hipError_t e, const char* what) {
     (void)hipGetLastError();
     set_error("%s: %s", what, hipGetErrorString(e));
     return MC_E_CUDA;
+}
+
+bool trace_enabled() {
+    static const bool on = std::getenv("MC_ROCTX") != nullptr;
+    return on;
 }
 
 }  // namespace mckv

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include "error.h"
+#include "trace.h"
 #include "kv_common.h"
 #include "kv_internal.h"
 
@@ -107,6 +108,7 @@ __global__ void inv_freq_init_kernel(float* __restrict__ table, double theta) {
 
 extern "C" mc_status_t mc_kv_rope_inv_freq_init(float* d_table, double rope_theta,
                                                 void* stream) {
+    mckv::TraceRange trace_range("mc_kv_rope_inv_freq_init");
     if (d_table == nullptr || !(rope_theta > 0.0)) {
         mckv::set_error("mc_kv_rope_inv_freq_init: table=%p theta=%g",
                         (void*)d_table, rope_theta);
@@ -123,6 +125,7 @@ extern "C" mc_status_t mc_kv_rope_append(uint16_t* d_qkv, uint32_t tokens,
                                          uint16_t* d_kv_pool, mc_kv_layout_t layout,
                                          double rope_theta, const float* d_inv_freq,
                                          void* stream) {
+    mckv::TraceRange trace_range("mc_kv_rope_append");
     mckv::DevLayout ly;
     if (d_qkv == nullptr || d_base_pos == nullptr || d_page_table == nullptr ||
         d_kv_pool == nullptr || tokens == 0 || !mckv::layout_valid(layout, &ly) ||

@@ -77,6 +77,14 @@ def _bind():
                                             C.POINTER(C.c_uint32), C.POINTER(LayoutT),
                                             C.POINTER(_P), C.POINTER(_P)]),
         "mc_debug_session_seq": (C.c_int, [Handle, C.POINTER(C.c_int32), C.c_uint32]),
+        "mc_debug_session_arena_bytes": (C.c_size_t, [Handle]),
+        "mc_debug_session_attn_chunk": (C.c_uint32, [Handle]),
+        "mc_debug_breakdown_raw_segments": (C.c_int, [Handle]),
+        "mc_debug_breakdown_collect": (C.c_int, [Handle, C.POINTER(C.c_double), C.c_int]),
+        "mc_debug_batch_group_stats": (C.c_int, [Handle, C.POINTER(C.c_uint64),
+                                                 C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)]),
+        "mc_debug_batch_breakdown_collect": (C.c_int, [Handle, C.POINTER(C.c_double),
+                                                       C.c_int]),
     }
     for n, (r, a) in sig.items():
         f = getattr(L, n)
@@ -150,6 +158,23 @@ class Session:
         check(_bind().mc_debug_session_seq(self.h, out, n), "mc_debug_session_seq")
         return list(out)
 
+    def arena_bytes(self) -> int:
+        return int(_bind().mc_debug_session_arena_bytes(self.h))
+
+    def attn_chunk(self) -> int:
+        return int(_bind().mc_debug_session_attn_chunk(self.h))
+
+    def breakdown(self):
+        """Segment times (ms) of the last decode step, or an int status
+        (0 = MC_BREAKDOWN was not set at create, < 0 = error)."""
+        L = _bind()
+        n = L.mc_debug_breakdown_raw_segments(self.h)
+        if n <= 0:
+            return n
+        out = (C.c_double * n)()
+        r = L.mc_debug_breakdown_collect(self.h, out, n)
+        return list(out) if r == n else r
+
     def close(self):
         if self.h.impl:
             _bind().mc_session_destroy(self.h)
@@ -180,6 +205,20 @@ class BatchGroup:
         out = (C.c_int32 * n)()
         check(_bind().mc_batch_step(self.h, ids, n, cf, out), "mc_batch_step")
         return list(out)
+
+    def stats(self):
+        steps, us, members = C.c_uint64(), C.c_uint64(), C.c_uint32()
+        check(_bind().mc_debug_batch_group_stats(self.h, C.byref(steps), C.byref(us),
+                                                 C.byref(members)), "mc_debug_batch_group_stats")
+        return {"steps": steps.value, "decode_us": us.value, "members": members.value}
+
+    def breakdown(self):
+        """Per-bucket times (ms) of the last step, or an int status."""
+        L = _bind()
+        n = L.mc_debug_breakdown_bucket_count()
+        out = (C.c_double * n)()
+        r = L.mc_debug_batch_breakdown_collect(self.h, out, n)
+        return list(out) if r == n else r
 
     def close(self):
         if self.h.impl:

@@ -88,7 +88,7 @@ def test_allocator_oom_before_any_copy(kvm):
     a = kvm.PagedKvAllocator(T(), 4, 32)
     with pytest.raises(kvm.McError) as e:
         a.ensure_pages_for(129, stream=0)
-    assert e.value.status == 5 and "exhausted" in str(e.value)
+    assert e.value.status == 5 and "exhausted" in str(e.value)  # OOM message
     assert a.pages_owned() == 0
 
 

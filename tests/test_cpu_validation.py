@@ -134,3 +134,20 @@ def test_session_abi_null_handles(pkg):
     L.mc_session_destroy(null)
     L.mc_batch_group_destroy(null)
     assert L.mc_last_error()
+
+
+def test_debug_hooks_without_handles(pkg, lib):
+    """The debug hooks validate their handles without touching a device."""
+    assert lib.mc_debug_breakdown_bucket_count() == 3
+    assert lib.mc_debug_breakdown_bucket_name(0) == b"qkv(synthetic)"
+    assert lib.mc_debug_breakdown_bucket_name(3) is None
+    assert lib.mc_debug_breakdown_bucket_of(-1) == -1
+    lib.mc_debug_breakdown_collect.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+    assert lib.mc_debug_breakdown_collect(None, None, 0) == -1
+    lib.mc_debug_batch_breakdown_collect.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+    assert lib.mc_debug_batch_breakdown_collect(None, None, 3) == -1
+    lib.mc_debug_batch_group_stats.argtypes = [C.c_void_p] * 4
+    assert lib.mc_debug_batch_group_stats(None, None, None, None) == INV
+    lib.mc_debug_session_arena_bytes.restype = C.c_size_t
+    lib.mc_debug_session_arena_bytes.argtypes = [C.c_void_p]
+    assert lib.mc_debug_session_arena_bytes(None) == 0

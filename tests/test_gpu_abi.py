@@ -381,3 +381,57 @@ def test_many_resets_and_two_threads(rt, tmp_path):
         assert ss[i].seq(len(prompts[i]) + 40) == solo[i][1]
         ss[i].close()
     m.close()
+
+
+@pytest.mark.parametrize("graphs", [0, 1])
+def test_breakdown_and_group_stats(rt, tmp_path, graphs, monkeypatch):
+    """The decode-step breakdown hooks (MC_BREAKDOWN / MC_BATCH_BREAKDOWN at
+    create, reference session.cpp:686-723, batch_group.cpp:869-927): off by
+    default (0), then one segment per (layer, {qkv, attention}) plus the tail,
+    all positive and summing to at most the step's wall time; the batch
+    group's bucket times and step statistics. With the step captured in a
+    HIP graph no segment is recorded (-2) and the statistics still count."""
+    import time
+    m = rt.Model(str(tmp_path), rt.model_options(max_context_tokens=2048, max_sessions=4,
+                                                 enable_cuda_graph=graphs))
+    plain = rt.Session(m)
+    assert plain.breakdown() == 0 and plain.arena_bytes() > 0 and plain.attn_chunk() == 64
+    monkeypatch.setenv("MC_BREAKDOWN", "1")
+    monkeypatch.setenv("MC_BATCH_BREAKDOWN", "1")
+    s = rt.Session(m)
+    s.prefill(list(range(5, 300)))
+    cfg = rt.gen_config(max_new_tokens=50, seed=2)
+    assert s.breakdown() == -2  # no decode step yet
+    for _ in range(3):
+        t0 = time.perf_counter()
+        s.decode_one(cfg)
+        wall_ms = (time.perf_counter() - t0) * 1e3
+        segs = s.breakdown()
+        if graphs:
+            assert segs == -2
+            continue
+        assert isinstance(segs, list) and len(segs) == 2 * 42 + 1
+        assert all(x >= 0.0 for x in segs) and sum(segs) <= wall_ms + 0.05
+        assert all(x > 0.0 for x in segs[1:84:2])  # the attention segments
+    L = rt._bind()
+    assert L.mc_debug_breakdown_bucket_count() == 3
+    assert L.mc_debug_breakdown_bucket_name(1).startswith(b"attn")
+    assert L.mc_debug_breakdown_bucket_of(1) == 1 and L.mc_debug_breakdown_bucket_of(84) == 2
+    g = rt.BatchGroup(m, 4, 2048)
+    assert g.breakdown() == -2
+    slot = g.add(s)
+    for k in range(4):
+        g.step([slot], [cfg])
+        st = g.stats()
+        assert st["steps"] == k + 1 and st["members"] == 1 and st["decode_us"] > 0
+        b = g.breakdown()
+        if graphs:
+            assert b == -2
+            continue
+        assert isinstance(b, list) and len(b) == 3 and b[1] > 0.0 and min(b) >= 0.0
+    g.remove(slot)
+    assert g.stats()["members"] == 0
+    g.close()
+    s.close()
+    plain.close()
+    m.close()
