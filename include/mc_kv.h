@@ -156,6 +156,22 @@ mc_status_t mc_kv_attention_decode(const uint16_t* d_q_rows, const uint32_t* d_p
                                    const float* d_inv_freq, uint32_t chunk_pos,
                                    float* d_partials2);
 
+/* Allocation-free decode. No counterpart in the reference: it is for callers
+ * that cannot allocate or pass scratch (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). Same computation and
+ * output as mc_kv_attention_decode (bit-identical), but the records live in
+ * a library-owned device array of 16 x 256 x 130 floats (2.13 MB per device,
+ * held until the process ends), so no d_partials / d_partials2 are taken and
+ * nothing is allocated. Limit: at most 256 records per head, i.e. chunk_pos a
+ * multiple of 64 or max_chunks <= 256 (else MC_E_INVALID_ARGUMENT). All calls
+ * on one device share the array: calls that overlap on a device (e.g. on two
+ * streams) race and must be serialized by the caller. */
+mc_status_t mc_kv_attention_decode_noalloc(const uint16_t* d_q_rows, const uint32_t* d_pos,
+                                           uint32_t layer, const uint32_t* d_page_table,
+                                           uint16_t* d_kv_pool, mc_kv_layout_t layout,
+                                           uint32_t max_chunks, uint16_t* d_out, void* stream,
+                                           const float* d_inv_freq, uint32_t chunk_pos);
+
 /* launch_attention_decode_merge (kernels.h:394-400): merge only, from given
  * level-1 partials. */
 mc_status_t mc_kv_attention_decode_merge(const float* d_partials,

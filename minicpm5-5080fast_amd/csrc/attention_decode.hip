@@ -17,6 +17,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 
 #include "decode_kernels.h"
 #include "error.h"
@@ -419,10 +420,83 @@ mc_status_t run_decode(ChunkLaunch L, float* partials2) {
                                partials2, L.out, L.st);
 }
 
+// ---- allocation-free decode: records in a library-owned device array ----
+//
+// mc_kv_attention_decode_noalloc keeps its records in `scratch`, a file-scope
+// device array of kScratchFloats floats (16 heads x 256 records x 130 =
+// 2.13 MB on every device the library runs on, held until the process ends).
+// The array's name is only a host-side stand-in: the device address is taken
+// once per device with hipGetSymbolAddress (device current) and that pointer
+// is what the kernels receive. Every call on one device shares the array, so
+// calls that overlap on a device race; the records need no clearing (a merge
+// reads only the records its call wrote).
+constexpr size_t kScratchFloats = (size_t)kHq * kMaxRanges * kPartial;
+__device__ __align__(256) float scratch[kScratchFloats];
+
+// Device address of `scratch` on the current device, looked up once per
+// device; nullptr (error set) when the lookup fails.
+float* scratch_ptr() {
+    static std::mutex mu;
+    static float* ptrs[64] = {};
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) {
+        if (e != hipSuccess) (void)hipGetLastError();
+        set_error("mc_kv_attention_decode_noalloc: no usable current device (%d)", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            set_error("mc_kv_attention_decode_noalloc: hipGetSymbolAddress(scratch) failed on "
+                      "device %d: %s",
+                      dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        ptrs[dev] = static_cast<float*>(p);
+    }
+    return ptrs[dev];
+}
+
 }  // namespace
 }  // namespace mckv
 
 using namespace mckv;
+
+extern "C" mc_status_t mc_kv_attention_decode_noalloc(
+    const uint16_t* d_q_rows, const uint32_t* d_pos, uint32_t layer,
+    const uint32_t* d_page_table, uint16_t* d_kv_pool, mc_kv_layout_t layout,
+    uint32_t max_chunks, uint16_t* d_out, void* stream, const float* d_inv_freq,
+    uint32_t chunk_pos) {
+    mckv::TraceRange trace_range("mc_kv_attention_decode_noalloc");
+    DevLayout ly;
+    if (d_q_rows == nullptr || d_pos == nullptr || d_page_table == nullptr ||
+        d_kv_pool == nullptr || d_out == nullptr || !layout_valid(layout, &ly) ||
+        layer >= layout.num_layers || !chunk_args_ok(max_chunks, chunk_pos)) {
+        set_error("mc_kv_attention_decode_noalloc: invalid args (layer=%u max_chunks=%u "
+                  "chunk_pos=%u)",
+                  layer, max_chunks, chunk_pos);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    const uint32_t cpw = chunks_per_range(max_chunks, chunk_pos);
+    const uint32_t nr = (max_chunks + cpw - 1u) / cpw;
+    if (nr > kMaxRanges) {
+        set_error("mc_kv_attention_decode_noalloc: %u records per head exceed the %u the "
+                  "built-in scratch holds (chunk_pos=%u is not a multiple of 64 and "
+                  "max_chunks=%u > %u); use mc_kv_attention_decode",
+                  nr, kMaxRanges, chunk_pos, max_chunks, kMaxRanges);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    float* rec = scratch_ptr();
+    if (rec == nullptr) return MC_E_CUDA;
+    ChunkLaunch L{d_q_rows, d_pos, nullptr, 1u, layer, d_page_table, nullptr, d_kv_pool,
+                  nullptr, ly, rec, max_chunks, 0u, d_out, (hipStream_t)stream,
+                  d_inv_freq, chunk_pos, 0u, false};
+    return run_decode<false>(L, nullptr);
+}
 
 extern "C" mc_status_t mc_kv_attention_decode_chunks(
     const uint16_t* d_q_rows, const uint32_t* d_pos, uint32_t layer,

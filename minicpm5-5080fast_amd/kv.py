@@ -99,6 +99,18 @@ def launch_attention_decode(d_q_rows, d_pos, layer, d_page_table, d_kv_pool,
                                        _ptr(d_partials2)), "launch_attention_decode")
 
 
+def launch_attention_decode_noalloc(d_q_rows, d_pos, layer, d_page_table, d_kv_pool,
+                                    layout: KvLayout, max_chunks, d_out, stream=None,
+                                    d_inv_freq=None, chunk_pos=64) -> None:
+    """Decode without caller scratch (records in a library-owned device array;
+    calls overlapping on one device race). No reference counterpart."""
+    check(lib().mc_kv_attention_decode_noalloc(_ptr(d_q_rows), _ptr(d_pos), layer,
+                                               _ptr(d_page_table), _ptr(d_kv_pool),
+                                               layout.c(), max_chunks, _ptr(d_out),
+                                               _stream(stream), _ptr(d_inv_freq), chunk_pos),
+          "launch_attention_decode_noalloc")
+
+
 def launch_attention_decode_chunks(d_q_rows, d_pos, layer, d_page_table, d_kv_pool,
                                    layout: KvLayout, d_partials, max_chunks, d_out,
                                    stream=None, d_inv_freq=None, chunk_pos=64) -> None:
