@@ -113,8 +113,13 @@ constexpr uint32_t kKv2MinBlocks = 256;
 // Register tiles in each wave's load ring (one load group ahead).
 constexpr uint32_t kRing = 2;
 
+// K/V rows are read once per launch: non-temporal loads keep them from
+// displacing cached data (page tables, records) on their way through
+// (C4 30.8 -> 30.0, C3 13.5 -> 12.6, C1 8.35 -> 7.9 us/layer).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
-    return *reinterpret_cast<const uint4*>(p);
+    return __builtin_bit_cast(uint4,
+                              __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
 }
 
 struct Tile {
