@@ -46,7 +46,28 @@ def parse():
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (eager launches)")
     ap.add_argument("--calib", action="store_true",
                     help="also run one 256 MiB device copy (PMC byte calibration)")
+    ap.add_argument("--decode-timeline", action="store_true",
+                    help="attach the decode timeline hook (in-kernel clock stamps) and add "
+                         "a per-layer timeline to each decode result")
     return ap.parse_args()
+
+
+# Decode timeline buffer (--decode-timeline): TIMELINE_LAUNCHES regions, attached
+# before any decode is captured.
+TIMELINE = None
+TIMELINE_LAUNCHES = 64
+
+
+def timeline_of(kvm, torch, step):
+    """Replays `step` once with the timeline buffer cleared and summarizes the
+    decodes it ran (None without --decode-timeline)."""
+    if TIMELINE is None:
+        return None
+    TIMELINE.zero_()
+    torch.cuda.synchronize()
+    step()
+    torch.cuda.synchronize()
+    return kvm.timeline_summary(TIMELINE.cpu().numpy())
 
 
 class Timer:
@@ -169,9 +190,11 @@ def bench_decode_single(kvm, torch, dev, timer, ctx, steps, warmup, rot):
     ms_med = timer.median(step)
     timer.run(chunks_only, max(1, warmup))
     ms_chunk = timer.run(chunks_only, steps)
+    tl = timeline_of(kvm, torch, step)
     bytes_layer = ctx * KV_BYTES_PER_TOKEN + QO_BYTES
     del pools
     return {
+        **({"timeline_us": tl} if tl else {}),
         "ctx": ctx, "sessions": 1, "chunk_pos": C, "pages_per_layer": npages,
         "ms_per_step": ms, "us_per_layer": ms * 1e3 / LAYERS,
         "us_per_layer_median30": ms_med * 1e3 / LAYERS,
@@ -218,8 +241,10 @@ def bench_decode_batch(kvm, torch, dev, timer, B, ctx, steps, warmup):
     timer.run(step, warmup)
     ms = timer.run(step, steps)
     ms_med = timer.median(step)
+    tl = timeline_of(kvm, torch, step)
     bytes_layer = B * (ctx * KV_BYTES_PER_TOKEN + QO_BYTES)
     return {
+        **({"timeline_us": tl} if tl else {}),
         "ctx": ctx, "sessions": B, "chunk_pos": C, "ms_per_step": ms,
         "us_per_layer": ms * 1e3 / LAYERS,
         "us_per_layer_median30": ms_med * 1e3 / LAYERS,
@@ -299,9 +324,11 @@ def bench_churn(kvm, torch, dev, timer, steps=64, B=8, max_ctx=131072, seed=5):
         for s in range(B):
             lens[s] += 1
     wall = time.perf_counter() - t0
+    tl = timeline_of(kvm, torch, step)
     alloc.close()
     kv_bytes = kv_tokens * KV_BYTES_PER_TOKEN * LAYERS
     return {
+        **({"timeline_us": tl} if tl else {}),
         "sessions": B, "steps": steps, "max_ctx": max_ctx, "chunk_pos": C,
         "mean_ctx": kv_tokens / steps / B,
         "gpu_us_per_layer": gpu_ms * 1e3 / steps / LAYERS,
@@ -336,8 +363,21 @@ def bench_append(kvm, torch, dev, timer, T, steps, warmup):
     kv_bytes = T * 512 * 2 * 2  # k,v read + page write
     q_bytes = T * 2048 * 2 * 2  # q read + write (rotated in place)
     us = ms * 1e3 / LAYERS
+
+    # Copy ceiling: torch's in-place elementwise multiply over the same qkv
+    # rows moves the same bytes (every row read once and written once).
+    rows = qkv.view(torch.bfloat16)
+
+    def ceil_f():
+        for l in range(LAYERS):
+            rows[l * T * 2560:(l + 1) * T * 2560].mul_(1.0)
+
+    ceil_step = timer.capture([ceil_f])
+    timer.run(ceil_step, warmup)
+    ceil_us = timer.run(ceil_step, steps) * 1e3 / LAYERS
     return {
         "tokens": T, "us_per_layer": us, "ms_per_step": ms,
+        "torch_inplace_mul_same_bytes_us": ceil_us,
         "kv_bytes_per_layer": kv_bytes, "all_bytes_per_layer": kv_bytes + q_bytes,
         "gbs_incl_q": (kv_bytes + q_bytes) / (us * 1e-6) / 1e9,
         "pct_hbm_peak_incl_q": 100.0 * (kv_bytes + q_bytes) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
@@ -525,6 +565,11 @@ def main():
     kvm = pkg.kv
     dev = torch.device("cuda:0")
     timer = Timer(torch, graphs=not args.eager)
+    if args.decode_timeline:
+        global TIMELINE
+        TIMELINE = torch.zeros(TIMELINE_LAUNCHES * kvm.TIMELINE_WORDS, dtype=torch.int64,
+                               device=dev)
+        kvm.debug_decode_timeline(TIMELINE, TIMELINE_LAUNCHES)
     cfgs = [c.strip() for c in args.configs.split(",") if c.strip()]
     res = {}
     if "c4" in cfgs:

@@ -325,6 +325,20 @@ mc_status_t mc_kv_debug_decode_fp32p(uint32_t fp32_p, uint32_t* previous);
  * value goes to *previous when not NULL. No reference counterpart. */
 mc_status_t mc_kv_debug_decode_records_only(uint32_t enable, uint32_t* previous);
 
+/* Debug timeline (process-wide, default off): attaches a device buffer of
+ * launches * MC_KV_TIMELINE_WORDS uint64 words. Each later decode
+ * (mc_kv_attention_decode, _batch, _noalloc) takes the next region of the
+ * ring; in its region, chunk-kernel workgroup w (w < 8192, linear block
+ * index) writes words 4w..4w+3 = {entry clock, exit clock (latest wave),
+ * XCC id, 0} and merge workgroup m (m < 2048) writes words 32768 + 2m..+1 =
+ * {entry, exit}. The clock is s_memrealtime, 100 MHz. The caller zeroes the
+ * buffer; unwritten words stay 0. A captured graph keeps the regions it was
+ * captured with. d_stamps = NULL with launches = 0 detaches (the region
+ * counter restarts at 0 on every call). Detached, the kernels only test a
+ * null pointer. No reference counterpart. */
+#define MC_KV_TIMELINE_WORDS 36864u
+mc_status_t mc_kv_debug_decode_timeline(uint64_t* d_stamps, uint32_t launches);
+
 /* Library build identity, e.g. "minicpm-kv gfx950". */
 const char* mc_kv_build_info(void);
 

@@ -80,6 +80,7 @@ _SIGS = {
     "mc_debug_breakdown_bucket_name": (C.c_char_p, [C.c_int]),
     "mc_debug_breakdown_bucket_of": (C.c_int, [C.c_int]),
     "mc_kv_debug_decode_records_only": (C.c_int, [_u32, _P]),
+    "mc_kv_debug_decode_timeline": (C.c_int, [_P, _u32]),
 }
 
 

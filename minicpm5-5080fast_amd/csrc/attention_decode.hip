@@ -172,7 +172,8 @@ template <bool BATCH>
 __global__ void __launch_bounds__(128) merge_b_kernel(
     const float* __restrict__ partials2, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, unsigned long long* stamps) {
+    const WgStamp stamp(stamps, blockIdx.x, 2u, kTlMergeWgs);
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
     Loaded<kSplit2> x;
     const float* base = partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial;
@@ -194,7 +195,8 @@ template <bool BATCH, uint32_t NMAX>
 __global__ void __launch_bounds__(128) merge_p_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, unsigned long long* stamps) {
+    const WgStamp stamp(stamps, blockIdx.x, 2u, kTlMergeWgs);
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
     const float* base = partials + ((size_t)slot * kHq + qh) * NC * kPartial;
     float M, L, A;
@@ -226,7 +228,8 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
 template <bool BATCH>
 mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
                          const uint32_t* const* slot_pos, uint32_t B, uint32_t NC,
-                         uint32_t C, float* partials2, uint16_t* out, hipStream_t st) {
+                         uint32_t C, float* partials2, uint16_t* out, hipStream_t st,
+                         unsigned long long* stamps) {
     // With at most 32 chunks every level-2 split holds one chunk, merge_a would
     // copy it exactly (m, l * 1, acc * 1), and merge_b's ascending fold equals
     // the one-level fold: a single kernel gives the identical result.
@@ -240,13 +243,13 @@ mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
             hipLaunchKernelGGL((merge_a_kernel<BATCH, 64u>), ga, dim3(128), 0, st, partials,
                                d_pos, slot_pos, NC, C, partials2);
         hipLaunchKernelGGL((merge_b_kernel<BATCH>), dim3(B * kHq), dim3(128), 0, st,
-                           partials2, d_pos, slot_pos, NC, C, out);
+                           partials2, d_pos, slot_pos, NC, C, out, stamps);
     } else if (NC <= kSplit2) {
         hipLaunchKernelGGL((merge_p_kernel<BATCH, kSplit2>), dim3(B * kHq), dim3(128), 0, st,
-                           partials, d_pos, slot_pos, NC, C, out);
+                           partials, d_pos, slot_pos, NC, C, out, stamps);
     } else {
         hipLaunchKernelGGL((merge_p_kernel<BATCH, 0u>), dim3(B * kHq), dim3(128), 0, st,
-                           partials, d_pos, slot_pos, NC, C, out);
+                           partials, d_pos, slot_pos, NC, C, out, stamps);
     }
     return check_launch("decode attention merge launch failed");
 }
@@ -267,7 +270,8 @@ template <bool BATCH, uint32_t Q, uint32_t RPT>
 __global__ void __launch_bounds__(256) merge_r_kernel(
     const float* __restrict__ rec, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NR, uint32_t C_rng,
-    uint32_t pos_max, uint16_t* __restrict__ out) {
+    uint32_t pos_max, uint16_t* __restrict__ out, unsigned long long* stamps) {
+    const WgStamp stamp(stamps, blockIdx.x + gridDim.x * blockIdx.y, 2u, kTlMergeWgs);
     static_assert(Q == 1u || Q == 2u || Q == 4u || Q == 8u, "dim quads per block");
     constexpr uint32_t kSlices = 32u / Q;  // blocks per head
     constexpr uint32_t kLanes = 256u / Q;
@@ -351,7 +355,7 @@ void launch_merge_r(const ChunkLaunch& L, uint32_t NR) {
     const uint32_t C_rng = L.C * L.cpw, pmax = pool_pos_max(L.ly);
 #define MC_MERGE_R(QQ, RR)                                                                  \
     hipLaunchKernelGGL((merge_r_kernel<BATCH, QQ, RR>), grid, dim3(256), 0, L.st, L.partials, \
-                       L.d_pos, L.slot_pos, NR, C_rng, pmax, L.out)
+                       L.d_pos, L.slot_pos, NR, C_rng, pmax, L.out, merge_stamps(L.stamps))
     if (rpt <= 1u) MC_MERGE_R(8u, 1u);
     else if (rpt <= 2u) MC_MERGE_R(8u, 2u);
     else if (rpt <= 4u) MC_MERGE_R(8u, 4u);
@@ -394,6 +398,21 @@ bool fp32p_on() {
 // kernel, so its time can be taken alone in the production configuration.
 std::atomic<uint32_t> g_records_only{0u};
 
+// Debug timeline buffer: run_decode gives each decode the next of `launches`
+// regions of kTlWordsPerLaunch words, in a ring (mc_kv_debug_decode_timeline).
+// A captured graph keeps the regions it was captured with.
+std::mutex g_tl_mu;
+unsigned long long* g_tl_buf = nullptr;
+uint32_t g_tl_launches = 0u, g_tl_next = 0u;
+static_assert(kTlWordsPerLaunch == MC_KV_TIMELINE_WORDS, "timeline region size in mc_kv.h");
+unsigned long long* next_timeline_region() {
+    std::lock_guard<std::mutex> lk(g_tl_mu);
+    if (g_tl_buf == nullptr) return nullptr;
+    unsigned long long* r = g_tl_buf + (size_t)g_tl_next * kTlWordsPerLaunch;
+    g_tl_next = (g_tl_next + 1u) % g_tl_launches;
+    return r;
+}
+
 // Runs one decode: the chunk kernel writes one record per (range, query
 // head), or the output when the context fits one range; a merge kernel folds
 // the records: merge_p for at most 32 records per head, merge_r_kernel up to
@@ -405,6 +424,7 @@ mc_status_t run_decode(ChunkLaunch L, float* partials2) {
     L.cpw = chunks_per_range(L.NC, L.C);
     const uint32_t nr_max = (L.NC + L.cpw - 1u) / L.cpw;
     L.rec_stride = nr_max;
+    L.stamps = next_timeline_region();
     const mc_status_t st =
         fp32p_on() ? launch_chunk_kernel<true>(L) : launch_chunk_kernel<false>(L);
     if (st != MC_OK || g_records_only.load(std::memory_order_relaxed) != 0u) return st;
@@ -417,7 +437,7 @@ mc_status_t run_decode(ChunkLaunch L, float* partials2) {
         return check_launch("decode attention merge launch failed");
     }
     return launch_merge<BATCH>(L.partials, L.d_pos, L.slot_pos, L.B, nr_max, L.C * L.cpw,
-                               partials2, L.out, L.st);
+                               partials2, L.out, L.st, merge_stamps(L.stamps));
 }
 
 // ---- allocation-free decode: records in a library-owned device array ----
@@ -556,7 +576,7 @@ extern "C" mc_status_t mc_kv_attention_decode_merge(
         return MC_E_INVALID_ARGUMENT;
     }
     return launch_merge<false>(d_partials, d_pos, nullptr, 1, max_chunks, chunk_pos,
-                               d_partials2, d_out, (hipStream_t)stream);
+                               d_partials2, d_out, (hipStream_t)stream, nullptr);
 }
 
 extern "C" mc_status_t mc_kv_attention_decode_batch(
@@ -588,6 +608,19 @@ extern "C" mc_status_t mc_kv_debug_decode_fp32p(uint32_t fp32_p, uint32_t* previ
     }
     const uint32_t prev = g_fp32p.exchange(fp32_p);
     if (previous != nullptr) *previous = prev;
+    return MC_OK;
+}
+
+extern "C" mc_status_t mc_kv_debug_decode_timeline(uint64_t* d_stamps, uint32_t launches) {
+    if ((d_stamps == nullptr) != (launches == 0u)) {
+        set_error("mc_kv_debug_decode_timeline: stamps=%p with launches=%u (both or neither)",
+                  (void*)d_stamps, launches);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lk(g_tl_mu);
+    g_tl_buf = reinterpret_cast<unsigned long long*>(d_stamps);
+    g_tl_launches = launches;
+    g_tl_next = 0u;
     return MC_OK;
 }
 

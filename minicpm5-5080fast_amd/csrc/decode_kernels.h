@@ -659,6 +659,39 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     *reinterpret_cast<float2*>(pw + 4 + d4) = make_float2(Acc[2], Acc[3]);
 }
 
+// Debug timeline (mc_kv_debug_decode_timeline): with a stamp buffer attached,
+// workgroup w of a launch writes, at 4 * w of the launch's chunk region,
+// {entry clock, exit clock, XCC id, 0}: thread 0 stores the entry when the
+// workgroup starts and every wave raises the exit to the clock at which it
+// leaves (a vector atomic max). The clock is s_memrealtime (100 MHz, one
+// count per 10 ns, common to all CUs). Workgroups past kTlChunkWgs are not
+// recorded. stamps == nullptr (the default) costs one uniform branch at
+// entry and at exit.
+constexpr uint32_t kTlChunkWgs = 8192;
+constexpr uint32_t kTlMergeWgs = 2048;
+constexpr uint32_t kTlWordsPerLaunch = 4u * kTlChunkWgs + 2u * kTlMergeWgs;
+
+struct WgStamp {
+    unsigned long long* p;
+    __device__ __forceinline__ WgStamp(unsigned long long* stamps, uint32_t wg,
+                                       uint32_t words, uint32_t cap)
+        : p(stamps != nullptr && wg < cap ? stamps + (size_t)words * wg : nullptr) {
+        if (p != nullptr && threadIdx.x == 0u) {
+            p[0] = __builtin_amdgcn_s_memrealtime();
+            if (words > 2u) p[2] = (unsigned long long)__builtin_amdgcn_s_getreg(6164);
+        }
+    }
+    __device__ __forceinline__ ~WgStamp() {
+        if (p != nullptr && (threadIdx.x & 63u) == 0u)
+            atomicMax(p + 1, (unsigned long long)__builtin_amdgcn_s_memrealtime());
+    }
+};
+
+// Merge region of a launch's timeline stamps (after the chunk region).
+inline unsigned long long* merge_stamps(unsigned long long* chunk_stamps) {
+    return chunk_stamps != nullptr ? chunk_stamps + 4u * kTlChunkWgs : nullptr;
+}
+
 // Records per head the record merge folds (chunks_per_range keeps ranges
 // at or below it).
 constexpr uint32_t kMaxRanges = 256;
@@ -675,11 +708,11 @@ __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
     return n > NC ? NC : n;
 }
 
-// grid = (ceil(NC / cpw), 2 kv heads (1 with KV2), B slots). Single-session
-// launches pass B = 1 and the direct pointers; batched launches resolve
-// per-slot pointers from device tables. Records of slot s start at
-// partials + s * 16 * rec_stride * 130 with a per-head stride of rec_stride
-// records (rec_stride >= the number of ranges, ceil(NC / cpw)).
+// grid = (ceil(NC / cpw), 2 kv heads (1 with KV2), B slots), one workgroup
+// per range. Single-session launches pass B = 1 and the direct pointers;
+// batched launches resolve per-slot pointers from device tables. Records of
+// slot s start at partials + s * 16 * rec_stride * 130 with a per-head stride
+// of rec_stride records (rec_stride >= the number of ranges, ceil(NC / cpw)).
 template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P>
 __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
     __attribute__((amdgpu_waves_per_eu(2))) decode_chunk_kernel(
@@ -688,11 +721,26 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
     const uint32_t* pt, const uint32_t* const* __restrict__ slot_pt,
     uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
     float* __restrict__ partials, uint32_t NC, uint32_t rec_stride, uint16_t* __restrict__ out,
-    const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw) {
+    const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw, uint32_t B,
+    unsigned long long* stamps) {
+    const WgStamp stamp(stamps, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                        4u, kTlChunkWgs);
     // Positions beyond the pool's capacity do not exist: a limit past it is
     // clamped, so page-table reads stay within its max_pages entries.
     const uint32_t pos_max = pool_pos_max(ly);
-    uint32_t slot = blockIdx.z, group = blockIdx.x, limit;
+    const uint32_t kvh = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : blockIdx.y;
+    auto run = [&](uint32_t slot, uint32_t group, uint32_t limit) {
+        DecodeArgs a;
+        a.q_row = q_rows + (size_t)slot * kRow;
+        a.limit = limit;
+        a.pt = BATCH ? slot_pt[slot] : pt;
+        a.pool = BATCH ? slot_kv[slot] : pool;
+        a.rec = partials + (size_t)slot * kHq * rec_stride * kPartial;
+        a.rec_stride = rec_stride;
+        a.out = out + (size_t)slot * kHq * kD;
+        decode_range_body<PH0, PAGE16, TPW, KV2, FP32P>(a, layer, ly, NC, inv_freq, C, kvh,
+                                                        group, cpw);
+    };
     if constexpr (BATCH) {
         // Work compaction: the (x, slot) workgroups are numbered densely over
         // the chunk groups that exist (slot by slot, ascending), so ragged
@@ -700,55 +748,40 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
         // between the working ones. Every wave derives the same mapping from
         // all slots' limits: lane s reads slot s's limit, a DPP scan gives
         // the running total of chunk groups, and the slot is the first one
-        // whose total exceeds this workgroup's index.
-        const uint32_t B = gridDim.z;
-        const uint32_t flat = blockIdx.x + gridDim.x * blockIdx.z;
+        // whose total exceeds this workgroup's number. (A grid of one
+        // residency round whose workgroups stride over the work was measured
+        // slower: whole ranges are too coarse to balance that way.)
         const uint32_t Cc = TPW > 0u ? 64u * TPW : C;  // 64 * TPW: a shift
         const bool cpw_pow2 = (cpw & (cpw - 1u)) == 0u;
         const uint32_t cpw_log2 = (uint32_t)__builtin_ctz(cpw);
         auto groups = [&](uint32_t nv) {
             return cpw_pow2 ? (nv + cpw - 1u) >> cpw_log2 : (nv + cpw - 1u) / cpw;
         };
-        {
-            const uint32_t lane = threadIdx.x & 63u;
-            uint32_t lim = 0u, cnt = 0u;
-            if (lane < B) {
-                lim = min(*slot_pos[lane], pos_max);
-                cnt = groups(n_valid_chunks(lim, Cc, NC));
-            }
-            // inclusive scan over the 64 lanes: row_shr 1, 2, 4, 8 within each
-            // 16-lane row, then row_bcast 15 (into rows 1, 3) and 31 (rows 2, 3)
-            uint32_t incl = cnt;
-            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x111, 0xF, 0xF, false);
-            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x112, 0xF, 0xF, false);
-            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x114, 0xF, 0xF, false);
-            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x118, 0xF, 0xF, false);
-            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x142, 0xA, 0xF, false);
-            incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x143, 0xC, 0xF, false);
-            slot = (uint32_t)__builtin_popcountll(
-                __builtin_amdgcn_ballot_w64(lane < B && incl <= flat));
-            if (slot < B) {
-                const uint32_t end = (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)slot);
-                const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)cnt, (int)slot);
-                group = flat - (end - c);
-                limit = (uint32_t)__builtin_amdgcn_readlane((int)lim, (int)slot);
-            }
+        const uint32_t lane = threadIdx.x & 63u;
+        uint32_t lim = 0u, cnt = 0u;
+        if (lane < B) {
+            lim = min(*slot_pos[lane], pos_max);
+            cnt = groups(n_valid_chunks(lim, Cc, NC));
         }
+        // inclusive scan over the 64 lanes: row_shr 1, 2, 4, 8 within each
+        // 16-lane row, then row_bcast 15 (into rows 1, 3) and 31 (rows 2, 3)
+        uint32_t incl = cnt;
+        incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x111, 0xF, 0xF, false);
+        incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x112, 0xF, 0xF, false);
+        incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x114, 0xF, 0xF, false);
+        incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x118, 0xF, 0xF, false);
+        incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x142, 0xA, 0xF, false);
+        incl += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)incl, 0x143, 0xC, 0xF, false);
+        const uint32_t n = blockIdx.x + gridDim.x * blockIdx.z;
+        const uint32_t slot = (uint32_t)__builtin_popcountll(
+            __builtin_amdgcn_ballot_w64(lane < B && incl <= n));
         if (slot >= B) return;  // past the last existing chunk group (uniform)
+        const uint32_t end = (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)slot);
+        const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)cnt, (int)slot);
+        run(slot, n - (end - c), (uint32_t)__builtin_amdgcn_readlane((int)lim, (int)slot));
     } else {
-        limit = min(*d_pos, pos_max);
+        run(0u, blockIdx.x, min(*d_pos, pos_max));
     }
-    DecodeArgs a;
-    a.q_row = q_rows + (size_t)slot * kRow;
-    a.limit = limit;
-    a.pt = BATCH ? slot_pt[slot] : pt;
-    a.pool = BATCH ? slot_kv[slot] : pool;
-    a.rec = partials + (size_t)slot * kHq * rec_stride * kPartial;
-    a.rec_stride = rec_stride;
-    a.out = out + (size_t)slot * kHq * kD;
-    const uint32_t kvh = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : blockIdx.y;
-    decode_range_body<PH0, PAGE16, TPW, KV2, FP32P>(a, layer, ly, NC, inv_freq, C, kvh, group,
-                                                    cpw);
 }
 
 }  // namespace
@@ -774,6 +807,7 @@ struct ChunkLaunch {
     uint32_t C;
     uint32_t cpw;
     bool batched;
+    unsigned long long* stamps;  // debug timeline: this launch's region, or nullptr
 };
 
 // Both KV heads in one 512-thread workgroup when that still gives every CU a
@@ -795,7 +829,7 @@ void launch_one(const ChunkLaunch& L) {
     hipLaunchKernelGGL((decode_chunk_kernel<PH0, BATCH, PAGE16, TPW, KV2, FP32P>), grid, block,
                        0, L.st, L.q, L.d_pos, L.slot_pos, L.layer, L.pt, L.slot_pt, L.pool,
                        L.slot_kv, L.ly, L.partials, L.NC, L.rec_stride, L.out, L.inv_freq, L.C,
-                       L.cpw);
+                       L.cpw, L.B, L.stamps);
 }
 
 template <bool PH0, bool BATCH, bool PAGE16, bool FP32P>

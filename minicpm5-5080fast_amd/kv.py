@@ -207,6 +207,66 @@ def debug_decode_records_only(enable: bool) -> bool:
     return bool(prev.value)
 
 
+TIMELINE_WORDS = 36864  # uint64 words per decode launch (MC_KV_TIMELINE_WORDS)
+TIMELINE_CHUNK_WGS = 8192
+TIMELINE_MERGE_WGS = 2048
+
+
+def debug_decode_timeline(d_stamps, launches: int) -> None:
+    """Attaches (or, with None / 0, detaches) the decode timeline buffer:
+    `launches` regions of TIMELINE_WORDS int64 words, one per decode in a
+    ring. The caller zeroes the buffer. Debug hook."""
+    check(lib().mc_kv_debug_decode_timeline(_ptr(d_stamps) if d_stamps is not None else None,
+                                            launches), "debug_decode_timeline")
+
+
+def timeline_summary(stamps) -> dict:
+    """Per-decode timeline from a filled timeline buffer (numpy int64 array of
+    launches * TIMELINE_WORDS words): the written regions ordered by chunk
+    entry, each giving the chunk span (first workgroup entry to last wave
+    exit), the median and latest workgroup entry, the per-XCC median exit
+    range, the gap to the merge's first entry, the merge span, and the gap to
+    the next decode's chunk entry. Clock counts are 10 ns; results in us."""
+    import numpy as np
+    st = np.asarray(stamps, dtype=np.int64).reshape(-1, TIMELINE_WORDS)
+    recs = []
+    for r in st:
+        ck = r[:4 * TIMELINE_CHUNK_WGS].reshape(-1, 4)
+        ck = ck[ck[:, 0] > 0]
+        if len(ck) == 0:
+            continue
+        mg = r[4 * TIMELINE_CHUNK_WGS:].reshape(-1, 2)
+        mg = mg[mg[:, 0] > 0]
+        recs.append((ck, mg))
+    recs.sort(key=lambda x: x[0][:, 0].min())
+    rows = []
+    for i, (ck, mg) in enumerate(recs):
+        a, b = ck[:, 0].min(), ck[:, 1].max()
+        xcc = [np.median(ck[ck[:, 2] == x, 1]) - a for x in np.unique(ck[:, 2])]
+        row = {"chunk_span": (b - a) / 100, "median_wg_end": (np.median(ck[:, 1]) - a) / 100,
+               "last_wg_entry": (ck[:, 0].max() - a) / 100,
+               "xcc_median_end": [min(xcc) / 100, max(xcc) / 100], "workgroups": len(ck)}
+        end = b
+        if len(mg):
+            row["gap_to_merge"] = (mg[:, 0].min() - b) / 100
+            row["merge_span"] = (mg[:, 1].max() - mg[:, 0].min()) / 100
+            end = mg[:, 1].max()
+        if i + 1 < len(recs):
+            row["gap_to_next"] = (recs[i + 1][0][:, 0].min() - end) / 100
+            row["decode_period"] = (recs[i + 1][0][:, 0].min() - a) / 100
+        rows.append(row)
+    out = {"decodes": len(rows)}
+    for k in ("chunk_span", "median_wg_end", "last_wg_entry", "gap_to_merge", "merge_span",
+              "gap_to_next", "decode_period"):
+        v = [r[k] for r in rows if k in r]
+        if v:
+            out[k] = round(float(np.median(v)), 3)
+    if rows:
+        out["xcc_median_end"] = [round(float(np.median([r["xcc_median_end"][j] for r in rows])), 3)
+                                 for j in (0, 1)]
+    return out
+
+
 def launch_decode_advance(d_seq, d_next_token, d_seq_len, stream=None) -> None:
     check(lib().mc_kv_decode_advance(_ptr(d_seq), _ptr(d_next_token), _ptr(d_seq_len),
                                      _stream(stream)), "launch_decode_advance")

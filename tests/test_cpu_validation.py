@@ -151,3 +151,8 @@ def test_debug_hooks_without_handles(pkg, lib):
     lib.mc_debug_session_arena_bytes.restype = C.c_size_t
     lib.mc_debug_session_arena_bytes.argtypes = [C.c_void_p]
     assert lib.mc_debug_session_arena_bytes(None) == 0
+    lib.mc_kv_debug_decode_timeline.argtypes = [C.c_void_p, C.c_uint32]
+    assert lib.mc_kv_debug_decode_timeline(None, 4) == INV
+    assert b"both or neither" in lib.mc_last_error()
+    assert lib.mc_kv_debug_decode_timeline(C.c_void_p(0x1000), 0) == INV
+    assert lib.mc_kv_debug_decode_timeline(None, 0) == 0  # detach: no device needed

@@ -583,3 +583,42 @@ def test_fp32p_decode_vs_oracle(kvm, orc, dev, B, C, ctx, ph0):
     tolerance of the double oracle, and batched == single."""
     with fp32p_mode(kvm, 1):
         _batch_case(kvm, orc, dev, B, C, ctx, ph0, seed=ctx + B, P=64)
+
+
+@pytest.mark.parametrize("ctx,C,nc_ctx,chunk_wgs,merge_wgs",
+                         [(600, 64, 600, 20, 16), (40000, 64, 131072, 512, 64)])
+def test_decode_timeline_hook(kvm, dev, ctx, C, nc_ctx, chunk_wgs, merge_wgs):
+    """With the timeline buffer attached, a decode records one stamp pair per
+    chunk-kernel and merge workgroup (entry <= exit, the chunk kernel ending
+    before the merge starts) in the first region of the ring, the outputs
+    stay bit-identical to a launch without it, and detaching stops the
+    stamps."""
+    import torch
+    rng = np.random.default_rng(ctx)
+    P, L, layer = 64, 1, 0
+    maxp = -(-ctx // P) + 1
+    pt = rng.permutation(maxp).astype(np.uint32)
+    pool = randn_bf16(rng, maxp * P * 512 * L, 0.3)
+    q = randn_bf16(rng, 2560, 1.0)
+    NC = kvm.attention_decode_max_chunks(nc_ctx, C)
+    ref, _, _ = run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, ctx - 1, C, NC)
+    buf = torch.zeros(3 * kvm.TIMELINE_WORDS, dtype=torch.int64, device=dev)
+    kvm.debug_decode_timeline(buf, 3)
+    try:
+        got, _, _ = run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, ctx - 1, C, NC)
+    finally:
+        kvm.debug_decode_timeline(None, 0)
+    assert np.array_equal(got, ref)
+    st = from_dev(buf, np.int64).reshape(3, kvm.TIMELINE_WORDS)
+    ck = st[0, :4 * kvm.TIMELINE_CHUNK_WGS].reshape(-1, 4)
+    mg = st[0, 4 * kvm.TIMELINE_CHUNK_WGS:].reshape(-1, 2)
+    assert (ck[:chunk_wgs, 0] > 0).all() and not ck[chunk_wgs:].any()
+    assert (ck[:chunk_wgs, 1] >= ck[:chunk_wgs, 0]).all()
+    assert (mg[:merge_wgs, 0] > 0).all() and not mg[merge_wgs:].any()
+    assert (mg[:merge_wgs, 1] >= mg[:merge_wgs, 0]).all()
+    assert mg[:merge_wgs, 0].min() >= ck[:chunk_wgs, 1].max()
+    assert not st[1:].any()
+    summ = kvm.timeline_summary(st)
+    assert summ["decodes"] == 1 and summ["chunk_span"] > 0 and summ["merge_span"] > 0
+    run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, ctx - 1, C, NC)
+    assert np.array_equal(from_dev(buf, np.int64).reshape(3, -1), st)
