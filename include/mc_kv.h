@@ -139,7 +139,9 @@ mc_status_t mc_kv_rope_append(uint16_t* d_qkv, uint32_t tokens,
  * chunk kernel folds each workgroup's range of ceil(max_chunks / 256) chunks
  * (one chunk when max_chunks <= 256, or when chunk_pos is not a multiple of
  * 64) into one record {m, l, acc[128]} per query head, and a merge kernel
- * folds the records (fixed order). Beyond 256 records per head (chunk_pos
+ * folds the records (fixed order). With 33..256 records per head each head's
+ * records are stored split (acc[n][128], then {m, l}[n]) in the same space;
+ * d_partials' contents are then not the reference's partial layout. Beyond 256 records per head (chunk_pos
  * not a multiple of 64 and more than 256 chunks) the reference's merges run
  * instead: two-level through d_partials2 ([16][32][130]) when it is not NULL
  * and there are more than 32 records, else one-level. If limit < the range

@@ -255,7 +255,7 @@ mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
 }
 
 
-// Fold of the decode records {m, l, acc[128]} of one (slot, query head,
+// Fold of the decode records (split layout) of one (slot, query head,
 // slice of 4Q dims) per 256-thread block: record lane rl = t / Q (of
 // 256 / Q lanes) holds records rl + k * lanes, k < RPT, dim quad q = t % Q
 // dims 4q..4q+3 of the slice. Every record slot of the buffer is loaded
@@ -282,14 +282,16 @@ __global__ void __launch_bounds__(256) merge_r_kernel(
     const uint32_t head = blockIdx.x / kSlices;
     const uint32_t q = t % Q, rl = t / Q;
     const uint32_t d = (blockIdx.x % kSlices) * 4u * Q + 4u * q;
+    // Split layout: the head's acc rows [NR][128], then its {m, l} pairs.
     const float* hb = rec + ((size_t)slot * kHq + head) * NR * kPartial;
+    const float* hml = hb + (size_t)NR * kD;
     float2 ml[RPT], a01[RPT], a23[RPT];
 #pragma unroll
     for (uint32_t k = 0; k < RPT; ++k) {
-        const float* base = hb + (size_t)min(rl + k * kLanes, NR - 1u) * kPartial;
-        ml[k] = *reinterpret_cast<const float2*>(base);
-        a01[k] = *reinterpret_cast<const float2*>(base + 2 + d);  // rows are 8-byte aligned
-        a23[k] = *reinterpret_cast<const float2*>(base + 4 + d);
+        const uint32_t r = min(rl + k * kLanes, NR - 1u);
+        ml[k] = *reinterpret_cast<const float2*>(hml + 2u * r);
+        a01[k] = *reinterpret_cast<const float2*>(hb + (size_t)r * kD + d);  // 8-byte aligned
+        a23[k] = *reinterpret_cast<const float2*>(hb + (size_t)r * kD + d + 2);
     }
     const uint32_t limit = min(BATCH ? *slot_pos[slot] : *d_pos, pos_max);  // as the chunk kernel
     const uint32_t nr = n_valid_chunks(limit, C_rng, NR);
@@ -424,6 +426,7 @@ mc_status_t run_decode(ChunkLaunch L, float* partials2) {
     L.cpw = chunks_per_range(L.NC, L.C);
     const uint32_t nr_max = (L.NC + L.cpw - 1u) / L.cpw;
     L.rec_stride = nr_max;
+    L.split = nr_max > kSplit2 && nr_max <= kMaxRanges;  // the records merge_r reads
     L.stamps = next_timeline_region();
     const mc_status_t st =
         fp32p_on() ? launch_chunk_kernel<true>(L) : launch_chunk_kernel<false>(L);

@@ -147,8 +147,10 @@ struct DecodeArgs {
     uint32_t limit;
     const uint32_t* pt;
     uint16_t* pool;
-    float* rec;       // this slot's records: [16][rec_stride][130]
+    float* rec;       // this slot's records: 16 heads x rec_stride x 130 floats
     uint32_t rec_stride;
+    bool split;       // record layout per head: false {m, l, acc[128]} rows,
+                      // true acc[rec_stride][128] then {m, l}[rec_stride]
     uint16_t* out;    // this slot: [2048]
 };
 
@@ -156,8 +158,9 @@ struct DecodeArgs {
 // 256 threads process chunks [c_first, c_end) of one (slot, kv head) as ONE
 // range: every wave keeps a single online-softmax state across all chunks of
 // the range, the 4 wave states are folded once at the end and written as one
-// record {m, l, acc[128]} per query head at rec[(qh * rec_stride + group)],
-// or, when the range is the only one (nvalid <= cpw), as the output
+// record per query head, {m, l, acc[128]} at rec[(qh * rec_stride + group)]
+// (the reference's partial layout) or, split, acc at row `group` and {m, l}
+// at pair `group` of the head's block (see DecodeArgs), or, when the range is the only one (nvalid <= cpw), as the output
 // bf16(acc / l). With KV2 the workgroup has 512 threads and threads 256-511
 // run the same body for the second KV head over the same chunks (own LDS).
 // Waves take tiles j = wave, wave+4, ... of each chunk (a chunk still bounds
@@ -653,6 +656,16 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                        (uint32_t)o[2] | ((uint32_t)o[3] << 16));
         return;
     }
+    if (a.split) {
+        float* blk = a.rec + (size_t)qh * a.rec_stride * kPartial;
+        float* pa = blk + (size_t)group * kD + d4;
+        *reinterpret_cast<float2*>(pa) = make_float2(Acc[0], Acc[1]);
+        *reinterpret_cast<float2*>(pa + 2) = make_float2(Acc[2], Acc[3]);
+        if (d4 == 0u)
+            *reinterpret_cast<float2*>(blk + (size_t)a.rec_stride * kD + 2u * group) =
+                make_float2(M, L);
+        return;
+    }
     float* pw = a.rec + ((size_t)qh * a.rec_stride + group) * kPartial;
     if (d4 == 0u) *reinterpret_cast<float2*>(pw) = make_float2(M, L);
     *reinterpret_cast<float2*>(pw + 2 + d4) = make_float2(Acc[0], Acc[1]);
@@ -721,7 +734,7 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
     const uint32_t* pt, const uint32_t* const* __restrict__ slot_pt,
     uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
     float* __restrict__ partials, uint32_t NC, uint32_t rec_stride, uint16_t* __restrict__ out,
-    const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw, uint32_t B,
+    const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw, uint32_t B, bool split,
     unsigned long long* stamps) {
     const WgStamp stamp(stamps, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
                         4u, kTlChunkWgs);
@@ -737,6 +750,7 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
         a.pool = BATCH ? slot_kv[slot] : pool;
         a.rec = partials + (size_t)slot * kHq * rec_stride * kPartial;
         a.rec_stride = rec_stride;
+        a.split = split;
         a.out = out + (size_t)slot * kHq * kD;
         decode_range_body<PH0, PAGE16, TPW, KV2, FP32P>(a, layer, ly, NC, inv_freq, C, kvh,
                                                         group, cpw);
@@ -807,6 +821,7 @@ struct ChunkLaunch {
     uint32_t C;
     uint32_t cpw;
     bool batched;
+    bool split;                  // split record layout (DecodeArgs)
     unsigned long long* stamps;  // debug timeline: this launch's region, or nullptr
 };
 
@@ -829,7 +844,7 @@ void launch_one(const ChunkLaunch& L) {
     hipLaunchKernelGGL((decode_chunk_kernel<PH0, BATCH, PAGE16, TPW, KV2, FP32P>), grid, block,
                        0, L.st, L.q, L.d_pos, L.slot_pos, L.layer, L.pt, L.slot_pt, L.pool,
                        L.slot_kv, L.ly, L.partials, L.NC, L.rec_stride, L.out, L.inv_freq, L.C,
-                       L.cpw, L.B, L.stamps);
+                       L.cpw, L.B, L.split, L.stamps);
 }
 
 template <bool PH0, bool BATCH, bool PAGE16, bool FP32P>
