@@ -81,6 +81,15 @@ _SIGS = {
     "mc_debug_breakdown_bucket_of": (C.c_int, [C.c_int]),
     "mc_kv_debug_decode_records_only": (C.c_int, [_u32, _P]),
     "mc_kv_debug_decode_timeline": (C.c_int, [_P, _u32]),
+    "mc_model_embedding_gather": (C.c_int, [_P, _P, _P, _P, _u32, _u32, _P]),
+    "mc_model_rmsnorm_rows": (C.c_int, [_P, _P, _P, _P, _u32, _u32, C.c_float, _P]),
+    "mc_model_swiglu_rows": (C.c_int, [_P, _P, _u32, _u32, _P]),
+    "mc_model_gemv": (C.c_int, [_P, _P, _u32, _P, _u32, _u32, _u32, _u32, _P]),
+    "mc_model_gemv_resnorm": (C.c_int, [_P, _P, _P, _P, _P, _u32, _P, _u32, _u32, _u32,
+                                        C.c_float, _P]),
+    "mc_model_gemv_swiglu": (C.c_int, [_P, _P, _u32, _P, _u32, _u32, _u32, _u32, _P]),
+    "mc_model_argmax_bf16": (C.c_int, [_P, _u32, _u32, _P, _P, _P]),
+    "mc_model_wpk_check": (C.c_int, [C.c_char_p, C.POINTER(C.c_uint64)]),
 }
 
 

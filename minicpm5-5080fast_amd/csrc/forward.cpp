@@ -1,0 +1,215 @@
+// forward.cpp - the MiniCPM5 forward over the paged KV cache when real
+// weights are loaded (model.wpk).
+//
+// Layer graph of the reference (native/runtime/forward.cpp:200-420):
+//   residual -> RMSNorm(norm1) -> qkv projection -> RoPE (q in place, k/v
+//   into the pages) -> paged causal GQA attention -> o projection ->
+//   residual add -> RMSNorm(norm2) -> gate_up projection -> SwiGLU -> down
+//   projection -> residual add -> RMSNorm(next layer's norm1, or final_norm
+//   after the last layer); logits of the last row through lm_head, greedy
+//   argmax into the next token. Every rounding point of the reference is kept:
+//   the residual is stored in bf16 after each add, norms, projections, SwiGLU
+//   and logits are bf16.
+//
+// MI355X mapping:
+//   * prefill (T rows): projections through rocBLAS GEMM (bf16 in/out, fp32
+//     compute), RMSNorm / residual-add kernels, SwiGLU, the paged prefill
+//     attention; the lm_head of the last row through the GEMV;
+//   * decode (one row) and batch steps (n <= 8 rows): every projection is the
+//     HBM-streaming GEMV of model_kernels.hip, with the residual add + RMSNorm
+//     fused into the GEMV that consumes it (qkv, gate_up, lm_head) and the
+//     SwiGLU fused into the down projection (the reference's fused decode
+//     chain, forward.cpp:165-190); the residual alternates between two
+//     buffers so that the workgroup writing the new residual never races the
+//     workgroups still reading the old one. Attention is the phase0 decode
+//     (RoPE + K/V append + split-KV attention in one chunk kernel).
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <utility>
+
+#include "error.h"
+#include "kv_common.h"
+#include "mc_kv.h"
+#include "model_internal.h"
+#include "trace.h"
+
+namespace mckv {
+namespace {
+
+constexpr double kTheta = 5.0e6;  // generated_model_config.h:23
+
+size_t a256(size_t x) { return (x + 255u) & ~size_t(255); }
+
+#define FWD_OR_RETURN(call)             \
+    do {                                \
+        const mc_status_t _s = (call);  \
+        if (_s != MC_OK) return _s;     \
+    } while (0)
+
+// y[M][N] = x[M][K] . W[N][K]^T through rocBLAS (column-major view: C(N x M) =
+// W^T(N x K) . x^T(K x M)).
+mc_status_t gemm_bf16(const Forward& f, const uint16_t* x, uint32_t M, const uint16_t* W,
+                      uint32_t N, uint32_t K, uint16_t* y) {
+    rocblas_handle h = static_cast<rocblas_handle>(f.blas);
+    if (rocblas_set_stream(h, f.st) != rocblas_status_success) {
+        set_error("prefill GEMM: rocblas_set_stream failed");
+        return MC_E_CUDA;
+    }
+    const float alpha = 1.f, beta = 0.f;
+    const rocblas_status s = rocblas_gemm_ex(
+        h, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
+        (rocblas_int)K, &alpha, W, rocblas_datatype_bf16_r, (rocblas_int)K, x,
+        rocblas_datatype_bf16_r, (rocblas_int)K, &beta, y, rocblas_datatype_bf16_r,
+        (rocblas_int)N, y, rocblas_datatype_bf16_r, (rocblas_int)N, rocblas_datatype_f32_r,
+        rocblas_gemm_algo_standard, 0, 0);
+    if (s != rocblas_status_success) {
+        set_error("prefill GEMM (%u x %u x %u): rocblas_gemm_ex failed: %s", M, N, K,
+                  rocblas_status_to_string(s));
+        return MC_E_CUDA;
+    }
+    return MC_OK;
+}
+
+}  // namespace
+
+size_t forward_act_bytes(uint32_t rows, uint32_t logit_rows) {
+    const size_t r = rows;
+    return a256(r * kHidden * 2u) * 2u      // res_a, res_b
+           + a256(r * kHidden * 2u)         // normed
+           + a256(r * kQkvCols * 2u)        // qkv
+           + a256(r * kHidden * 2u) * 2u    // attn, o_out
+           + a256(r * 2u * kInter * 2u)     // gate_up
+           + a256(r * kInter * 2u)          // mlp
+           + a256(r * kHidden * 2u)         // down
+           + a256((size_t)logit_rows * kVocabSize * 2u);
+}
+
+void forward_carve(Forward& f, char* p, uint32_t rows, uint32_t logit_rows) {
+    const size_t r = rows;
+    auto take = [&](size_t bytes) {
+        uint16_t* q = reinterpret_cast<uint16_t*>(p);
+        p += a256(bytes);
+        return q;
+    };
+    f.res_a = take(r * kHidden * 2u);
+    f.res_b = take(r * kHidden * 2u);
+    f.normed = take(r * kHidden * 2u);
+    f.qkv = take(r * kQkvCols * 2u);
+    f.attn = take(r * kHidden * 2u);
+    f.o_out = take(r * kHidden * 2u);
+    f.gate_up = take(r * 2u * kInter * 2u);
+    f.mlp = take(r * kInter * 2u);
+    f.down = take(r * kHidden * 2u);
+    f.logits = take((size_t)logit_rows * kVocabSize * 2u);
+    f.rows = rows;
+}
+
+mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, int32_t* d_next) {
+    TraceRange trace_range("forward_prefill");
+    const ModelWeights& w = *f.w;
+    hipStream_t st = f.st;
+    if (n == 0u || n > f.rows) {
+        set_error("forward_prefill: %u rows for buffers of %u", n, f.rows);
+        return MC_E_INTERNAL;
+    }
+    uint16_t* res = f.res_a;
+    FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, res, kHidden, n, st));
+    FWD_OR_RETURN(mc_model_rmsnorm_rows(res, nullptr, w.norm1[0], f.normed, n, kHidden, kRmsEps, st));
+    const uint32_t S = mc_kv_prefill_split_kv(n);
+    for (uint32_t l = 0; l < kModelLayers; ++l) {
+        FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.qkv[l], kQkvCols, kHidden, f.qkv));
+        FWD_OR_RETURN(mc_kv_rope_append(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout, kTheta,
+                                        f.inv_freq, st));
+        FWD_OR_RETURN(mc_kv_attention_prefill(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
+                                              f.attn, S > 1u ? f.pf_partials : nullptr, S, st));
+        FWD_OR_RETURN(gemm_bf16(f, f.attn, n, w.o[l], kHidden, kHidden, f.o_out));
+        FWD_OR_RETURN(
+            mc_model_rmsnorm_rows(res, f.o_out, w.norm2[l], f.normed, n, kHidden, kRmsEps, st));
+        FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.gate_up[l], 2u * kInter, kHidden, f.gate_up));
+        FWD_OR_RETURN(mc_model_swiglu_rows(f.gate_up, f.mlp, n, kInter, st));
+        FWD_OR_RETURN(gemm_bf16(f, f.mlp, n, w.down[l], kHidden, kInter, f.down));
+        const uint16_t* next_norm = l + 1u < kModelLayers ? w.norm1[l + 1u] : w.final_norm;
+        FWD_OR_RETURN(
+            mc_model_rmsnorm_rows(res, f.down, next_norm, f.normed, n, kHidden, kRmsEps, st));
+    }
+    FWD_OR_RETURN(mc_model_gemv(w.lm_head, f.normed + (size_t)(n - 1u) * kHidden, kHidden,
+                                f.logits, kVocabSize, 1, kVocabSize, kHidden, st));
+    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, st);
+}
+
+mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_next,
+                           const Marker& mark) {
+    TraceRange trace_range("forward_decode");
+    const ModelWeights& w = *f.w;
+    hipStream_t st = f.st;
+    // cur: the residual as of the current point; pending: the projection
+    // still to be added to it (none at layer 0).
+    uint16_t* cur = f.res_a;
+    uint16_t* other = f.res_b;
+    const uint16_t* pending = nullptr;
+    FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_tok, nullptr, cur, kHidden, 1, st));
+    for (uint32_t l = 0; l < kModelLayers; ++l) {
+        // qkv = W_qkv . norm1(cur + pending); the sum becomes the residual
+        FWD_OR_RETURN(mc_model_gemv_resnorm(w.qkv[l], cur, pending, w.norm1[l],
+                                            pending != nullptr ? other : nullptr, kHidden, f.qkv,
+                                            kQkvCols, 1, kQkvCols, kRmsEps, st));
+        if (pending != nullptr) std::swap(cur, other);
+        mark();
+        FWD_OR_RETURN(mc_kv_attention_decode(f.qkv, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
+                                             f.partials, f.max_chunks, f.attn, st, f.inv_freq,
+                                             f.chunk_pos, f.partials2));
+        FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn, kHidden, f.o_out, kHidden, 1, kHidden, kHidden,
+                                    st));
+        FWD_OR_RETURN(mc_model_gemv_resnorm(w.gate_up[l], cur, f.o_out, w.norm2[l], other, kHidden,
+                                            f.gate_up, 2u * kInter, 1, 2u * kInter, kRmsEps, st));
+        std::swap(cur, other);
+        FWD_OR_RETURN(mc_model_gemv_swiglu(w.down[l], f.gate_up, 2u * kInter, f.down, kHidden, 1,
+                                           kHidden, kInter, st));
+        pending = f.down;
+        mark();
+    }
+    FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur, pending, w.final_norm, nullptr, kHidden,
+                                        f.logits, kVocabSize, 1, kVocabSize, kRmsEps, st));
+    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, st);
+}
+
+mc_status_t forward_batch(const Forward& f, const BatchKv& b, const Marker& mark) {
+    TraceRange trace_range("forward_batch");
+    const ModelWeights& w = *f.w;
+    hipStream_t st = f.st;
+    const uint32_t n = b.n;
+    if (n == 0u || n > f.rows || n > MC_MODEL_GEMV_MAX_ROWS) {
+        set_error("forward_batch: %u rows for buffers of %u", n, f.rows);
+        return MC_E_INTERNAL;
+    }
+    uint16_t* cur = f.res_a;
+    uint16_t* other = f.res_b;
+    const uint16_t* pending = nullptr;
+    FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, nullptr, b.d_slot_tok, cur, kHidden, n, st));
+    for (uint32_t l = 0; l < kModelLayers; ++l) {
+        FWD_OR_RETURN(mc_model_gemv_resnorm(w.qkv[l], cur, pending, w.norm1[l],
+                                            pending != nullptr ? other : nullptr, kHidden, f.qkv,
+                                            kQkvCols, n, kQkvCols, kRmsEps, st));
+        if (pending != nullptr) std::swap(cur, other);
+        mark();
+        FWD_OR_RETURN(mc_kv_attention_decode_batch(f.qkv, b.d_slot_pos, n, l, b.d_slot_pt,
+                                                   b.d_slot_kv, f.layout, f.partials, f.max_chunks,
+                                                   f.attn, st, f.inv_freq, f.chunk_pos,
+                                                   f.partials2));
+        FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn, kHidden, f.o_out, kHidden, n, kHidden, kHidden,
+                                    st));
+        FWD_OR_RETURN(mc_model_gemv_resnorm(w.gate_up[l], cur, f.o_out, w.norm2[l], other, kHidden,
+                                            f.gate_up, 2u * kInter, n, 2u * kInter, kRmsEps, st));
+        std::swap(cur, other);
+        FWD_OR_RETURN(mc_model_gemv_swiglu(w.down[l], f.gate_up, 2u * kInter, f.down, kHidden, n,
+                                           kHidden, kInter, st));
+        pending = f.down;
+        mark();
+    }
+    FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur, pending, w.final_norm, nullptr, kHidden,
+                                        f.logits, kVocabSize, n, kVocabSize, kRmsEps, st));
+    return mc_model_argmax_bf16(f.logits, kVocabSize, n, nullptr, b.d_slot_tok, st);
+}
+
+}  // namespace mckv

@@ -1,0 +1,106 @@
+// model_internal.h - weight package and model constants shared by the host
+// translation units of the weight path (wpk.cpp, forward.cpp, abi_shell.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mc_kv.h"
+#include "mc_model.h"
+
+namespace mckv {
+
+// MiniCPM5-2B geometry (native/runtime/generated_model_config.h:13-23).
+constexpr uint32_t kModelLayers = 42;
+constexpr uint32_t kHidden = 2048;
+constexpr uint32_t kInter = 6144;
+constexpr uint32_t kVocabSize = 130560;
+constexpr uint32_t kQkvCols = 2560;  // q (16 x 128) | k (2 x 128) | v (2 x 128)
+constexpr float kRmsEps = 1e-6f;
+
+// Device pointers into one weight allocation (row-major bf16, [out][in]).
+struct ModelWeights {
+    void* arena = nullptr;
+    uint64_t bytes = 0;
+    const uint16_t* embedding = nullptr;   // [vocab][hidden]
+    const uint16_t* lm_head = nullptr;     // [vocab][hidden]
+    const uint16_t* final_norm = nullptr;  // [hidden]
+    const uint16_t* norm1[kModelLayers] = {};
+    const uint16_t* qkv[kModelLayers] = {};      // [2560][2048]
+    const uint16_t* o[kModelLayers] = {};        // [2048][2048]
+    const uint16_t* norm2[kModelLayers] = {};
+    const uint16_t* gate_up[kModelLayers] = {};  // [12288][2048], gate rows then up rows
+    const uint16_t* down[kModelLayers] = {};     // [2048][6144]
+};
+
+// Reads and checks `path` (a model.wpk). With `w` != nullptr the sections
+// are uploaded into one device allocation on the current device (stream
+// `st`), otherwise only checked; *arena_bytes receives the allocation size.
+mc_status_t wpk_load(const char* path, ModelWeights* w, uint64_t* arena_bytes, hipStream_t st);
+void wpk_free(ModelWeights* w);
+
+}  // namespace mckv
+
+namespace mckv {
+
+// Device buffers and KV state one forward works on. Activation buffers hold
+// `rows` rows; res_a / res_b are the two residual buffers the fused decode
+// chain alternates between.
+struct Forward {
+    const ModelWeights* w = nullptr;
+    hipStream_t st = nullptr;
+    void* blas = nullptr;  // rocblas_handle for the prefill GEMMs
+    // KV cache of a session (prefill and solo decode)
+    uint16_t* pool = nullptr;
+    const uint32_t* d_pt = nullptr;
+    mc_kv_layout_t layout{};
+    const uint32_t* d_seq_len = nullptr;  // positions are read here at run time
+    const float* inv_freq = nullptr;
+    float* partials = nullptr;
+    float* partials2 = nullptr;
+    float* pf_partials = nullptr;
+    uint32_t max_chunks = 0, chunk_pos = 64;
+    // activations
+    uint16_t *res_a = nullptr, *res_b = nullptr, *normed = nullptr, *qkv = nullptr,
+             *attn = nullptr, *o_out = nullptr, *gate_up = nullptr, *mlp = nullptr,
+             *down = nullptr, *logits = nullptr;
+    uint32_t rows = 0;
+};
+
+// Device bytes of the activation buffers of a Forward with `rows` rows and
+// `logit_rows` logits rows, and their carving from `base` (256-aligned).
+size_t forward_act_bytes(uint32_t rows, uint32_t logit_rows);
+void forward_carve(Forward& f, char* base, uint32_t rows, uint32_t logit_rows);
+
+// Prefill of n <= rows tokens at positions *d_seq_len.. (ids on the device):
+// K/V of every layer appended, the greedy next token written to *d_next.
+mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, int32_t* d_next);
+
+// Called at segment boundaries of a decode step (after each layer's qkv
+// projection and after the rest of the layer).
+struct Marker {
+    void (*fn)(void*) = nullptr;
+    void* ctx = nullptr;
+    void operator()() const {
+        if (fn != nullptr) fn(ctx);
+    }
+};
+
+// Decode of the token *d_tok at position *d_seq_len (K/V appended), the greedy
+// next token written to *d_next (may be d_tok).
+mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_next,
+                           const Marker& mark);
+
+// Batch decode of n <= 8 sessions: tokens *d_slot_tok[s], positions
+// *d_slot_pos[s], page tables d_slot_pt[s], pools d_slot_kv[s]; the next
+// tokens are written back to *d_slot_tok[s]. Activations of f (rows >= n).
+struct BatchKv {
+    const uint32_t* const* d_slot_pos;
+    const uint32_t* const* d_slot_pt;
+    uint16_t* const* d_slot_kv;
+    int32_t* const* d_slot_tok;
+    uint32_t n;
+};
+mc_status_t forward_batch(const Forward& f, const BatchKv& b, const Marker& mark);
+
+}  // namespace mckv

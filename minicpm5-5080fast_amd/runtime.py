@@ -12,6 +12,7 @@ from ._native import McError, check, lib, LayoutT
 
 MC_ABI_VERSION = 0x00020000
 EOS_STREAM_ID = 130073
+VOCAB = 130560
 
 
 class ModelOptions(C.Structure):
@@ -85,6 +86,8 @@ def _bind():
                                                  C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)]),
         "mc_debug_batch_breakdown_collect": (C.c_int, [Handle, C.POINTER(C.c_double),
                                                        C.c_int]),
+        "mc_debug_session_last_logits": (C.c_int, [Handle, C.POINTER(C.c_float)]),
+        "mc_debug_batch_last_logits": (C.c_int, [Handle, C.c_uint32, C.POINTER(C.c_float)]),
     }
     for n, (r, a) in sig.items():
         f = getattr(L, n)
@@ -164,6 +167,15 @@ class Session:
     def attn_chunk(self) -> int:
         return int(_bind().mc_debug_session_attn_chunk(self.h))
 
+    def last_logits(self):
+        """bf16 logits (as float32 numpy) of the session's last forward (a
+        model loaded with weights)."""
+        import numpy as np
+        out = np.empty(VOCAB, dtype=np.float32)
+        check(_bind().mc_debug_session_last_logits(
+            self.h, out.ctypes.data_as(C.POINTER(C.c_float))), "mc_debug_session_last_logits")
+        return out
+
     def breakdown(self):
         """Segment times (ms) of the last decode step, or an int status
         (0 = MC_BREAKDOWN was not set at create, < 0 = error)."""
@@ -211,6 +223,14 @@ class BatchGroup:
         check(_bind().mc_debug_batch_group_stats(self.h, C.byref(steps), C.byref(us),
                                                  C.byref(members)), "mc_debug_batch_group_stats")
         return {"steps": steps.value, "decode_us": us.value, "members": members.value}
+
+    def last_logits(self, slot: int):
+        """bf16 logits (as float32 numpy) of `slot` in the last step."""
+        import numpy as np
+        out = np.empty(VOCAB, dtype=np.float32)
+        check(_bind().mc_debug_batch_last_logits(
+            self.h, slot, out.ctypes.data_as(C.POINTER(C.c_float))), "mc_debug_batch_last_logits")
+        return out
 
     def breakdown(self):
         """Per-bucket times (ms) of the last step, or an int status."""

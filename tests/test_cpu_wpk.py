@@ -1,0 +1,208 @@
+"""model.wpk checks (mc_model_wpk_check, no device) and pins of the forward
+oracle (oracle/model_ref.py), on the CPU.
+
+The package checks follow the reference loader (weight_loader.cpp:201-330):
+header magic / ABI / target, TOC placement, unique name hashes, exactly the
+model's 255 sections, bf16 row-major tensors of the model's shapes, data
+inside the file. Packages here are sparse files (data holes), so the checks
+run on the full geometry without writing gigabytes.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import wpk_util as W
+
+OK, IO, MISMATCH, UNSUPPORTED = 0, 2, 4, 7
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg._native.lib()
+
+
+def check(lib, path):
+    n = C.c_uint64(0)
+    st = lib.mc_model_wpk_check(str(path).encode(), C.byref(n))
+    return st, n.value, lib.mc_last_error().decode()
+
+
+def test_valid_package(lib, tmp_path):
+    secs = W.model_sections()
+    p = tmp_path / "model.wpk"
+    W.write_wpk(p, secs, W.sparse_blobs())
+    st, n, msg = check(lib, p)
+    assert st == OK, msg
+    assert n == W.arena_bytes(secs)
+    # 2 x 535 MB tables + 42 x 94.4 MB layers + norms: the real model's size
+    assert 5.0e9 < n < 5.1e9
+
+
+@pytest.mark.parametrize("field,value", [("magic", 0x31504B4E), ("abi", 3), ("target_sm", 90),
+                                         ("toc_offset", 128), ("reserved", 1),
+                                         ("data_start", 1 << 40)])
+def test_bad_header(lib, tmp_path, field, value):
+    p = tmp_path / "model.wpk"
+    W.write_wpk(p, W.model_sections(), W.sparse_blobs(), header={field: value})
+    st, _, msg = check(lib, p)
+    assert st == MISMATCH and "model.wpk" in msg, msg
+
+
+def test_toc_longer_than_its_room(lib, tmp_path):
+    p = tmp_path / "model.wpk"
+    W.write_wpk(p, W.model_sections(), W.sparse_blobs(), header={"data_start": 64 + 132})
+    assert check(lib, p)[0] == MISMATCH
+
+
+def test_missing_file_and_short_header(lib, tmp_path):
+    assert check(lib, tmp_path / "none.wpk")[0] == IO
+    p = tmp_path / "model.wpk"
+    p.write_bytes(b"MKP1" + b"\x00" * 20)
+    assert check(lib, p)[0] == IO
+
+
+def test_section_count(lib, tmp_path):
+    p = tmp_path / "model.wpk"
+    secs = W.model_sections()
+    W.write_wpk(p, secs[:-1], W.sparse_blobs())  # one missing
+    st, _, msg = check(lib, p)
+    assert st == MISMATCH and "254" in msg, msg
+    extra = secs + [("layer42.norm1", (W.HIDDEN,), "final_norm")]
+    W.write_wpk(p, extra, W.sparse_blobs())
+    assert check(lib, p)[0] == MISMATCH
+
+
+def test_duplicate_and_unknown_names(lib, tmp_path):
+    p = tmp_path / "model.wpk"
+    secs = W.model_sections()
+
+    def dup(i, d):
+        if i == 7:
+            d["hash"] = W.fnv1a64("layer0.qkv")
+    W.write_wpk(p, secs, W.sparse_blobs(), entry_patch=dup)
+    st, _, msg = check(lib, p)
+    assert st == MISMATCH and "share" in msg, msg
+
+    def rename(i, d):
+        if i == 4:  # layer0.qkv
+            d["hash"] = W.fnv1a64("layer0.qkv_proj")
+    W.write_wpk(p, secs, W.sparse_blobs(), entry_patch=rename)
+    st, _, msg = check(lib, p)
+    assert st == MISMATCH and "layer0.qkv" in msg and "missing" in msg, msg
+
+
+@pytest.mark.parametrize("patch", [
+    lambda d: d.update(dtype=2), lambda d: d.update(layout=1), lambda d: d.update(rank=1),
+    lambda d: d["dims"].__setitem__(1, 2049), lambda d: d.update(bytes=d["bytes"] - 2),
+    lambda d: d.update(offset=64), lambda d: d.update(offset=1 << 42)])
+def test_bad_entry(lib, tmp_path, patch):
+    p = tmp_path / "model.wpk"
+
+    def ep(i, d):
+        if i == 10:  # layer1.qkv
+            patch(d)
+    W.write_wpk(p, W.model_sections(), W.sparse_blobs(), entry_patch=ep)
+    st, _, msg = check(lib, p)
+    assert st == MISMATCH and "layer1.qkv" in msg, msg
+
+
+def test_data_past_end_of_file(lib, tmp_path):
+    p = tmp_path / "model.wpk"
+    W.write_wpk(p, W.model_sections(), W.sparse_blobs())
+    size = os.path.getsize(p)
+    with open(p, "r+b") as f:
+        f.truncate(size - 4096)  # the last section now ends past the file
+    assert check(lib, p)[0] == MISMATCH
+
+
+def test_layer_window_switches_rejected(lib, tmp_path, monkeypatch):
+    p = tmp_path / "model.wpk"
+    W.write_wpk(p, W.model_sections(), W.sparse_blobs())
+    monkeypatch.setenv("MC_LOAD_LAYERS_MAX", "2")
+    st, _, msg = check(lib, p)
+    assert st == UNSUPPORTED and "MC_LOAD_LAYERS_MAX" in msg, msg
+
+
+# ---------------- pins of the forward oracle ----------------
+
+def test_rmsnorm_and_swiglu_closed_forms(orc):
+    from oracle import model_ref as M
+    rng = np.random.default_rng(3)
+    x = M.bf16(rng.standard_normal((3, 2048)).astype(np.float32) * 3)
+    w = M.bf16(1 + 0.1 * rng.standard_normal(2048).astype(np.float32))
+    ref = x.astype(np.float64) / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True)
+                                         + 1e-6) * w
+    got = M.rmsnorm(x, w)
+    assert np.all(np.abs(got - ref) <= orc.bf16_ulp(ref) * 0.5 + 1e-30)
+    # constant rows normalize to sign * w (up to eps)
+    c = np.full((1, 2048), 4.0, dtype=np.float32)
+    assert np.allclose(M.rmsnorm(c, w), M.bf16(w), rtol=2 ** -8)
+    g = np.array([-30.0, -1.0, 0.0, 1.0, 30.0], dtype=np.float32)
+    u = np.array([1.0, 2.0, 3.0, 4.0, 5.0], dtype=np.float32)
+    np.testing.assert_allclose(M.silu_mul(g, u), g / (1 + np.exp(-g.astype(np.float64))) * u,
+                               rtol=2 ** -8, atol=1e-12)
+
+
+def small_model(rng, vocab, layers, zero_mix=False):
+    """A model of the oracle's shapes with a small vocabulary."""
+    from oracle import model_ref as M
+
+    def mat(r, c, s):
+        return M.bf16(rng.standard_normal((r, c), dtype=np.float32) * np.float32(s))
+
+    w = {"embedding": mat(vocab, 2048, 1.0), "lm_head": mat(vocab, 2048, 1 / 45.25),
+         "final_norm": M.bf16(1 + 0.1 * rng.standard_normal(2048).astype(np.float32))}
+    for l in range(layers):
+        p = f"layer{l}."
+        w[p + "norm1"] = M.bf16(1 + 0.1 * rng.standard_normal(2048).astype(np.float32))
+        w[p + "norm2"] = M.bf16(1 + 0.1 * rng.standard_normal(2048).astype(np.float32))
+        w[p + "qkv"] = mat(2560, 2048, 1 / 45.25)
+        w[p + "gate_up"] = mat(12288, 2048, 1 / 45.25)
+        w[p + "o"] = np.zeros((2048, 2048), np.float32) if zero_mix else mat(2048, 2048, 1 / 45.25)
+        w[p + "down"] = (np.zeros((2048, 6144), np.float32) if zero_mix
+                         else mat(2048, 6144, 1 / 78.4))
+    return w
+
+
+def test_forward_with_zero_mixing_is_the_embedding_path(orc):
+    """With the o and down projections zero every layer adds nothing to the
+    residual: logits = bf16(rmsnorm(embedding[id], final_norm) . lm_head^T)
+    for every position, whatever the attention and MLP compute."""
+    from oracle import model_ref as M
+    rng = np.random.default_rng(5)
+    w = small_model(rng, 500, 2, zero_mix=True)
+    ref = M.ModelRef(w, 2)
+    ids = [3, 17, 499, 0]
+    tok = ref.forward(ids)
+    x = M.rmsnorm(w["embedding"][ids[-1]][None], w["final_norm"])
+    exact = (x.astype(np.float64) @ w["lm_head"].T.astype(np.float64))[0]
+    # the oracle accumulates in fp32: within one bf16 ulp of the exact product
+    assert np.all(np.abs(ref.last_logits - exact) <= orc.bf16_ulp(exact) + 1e-6)
+    assert tok == int(np.argmax(ref.last_logits))
+    assert exact[tok] >= exact.max() - 2 * orc.bf16_ulp(exact.max())
+    # decode: returns the pending prediction, then predicts from it
+    assert ref.decode() == tok and ref.seq_len == 5
+
+
+def test_forward_single_token_attention_is_v(orc):
+    """At position 0 the attention output is V of that position (one key):
+    the oracle's layer output equals the same graph with attention replaced
+    by the V columns of the rotated qkv row."""
+    from oracle import model_ref as M
+    rng = np.random.default_rng(7)
+    w = small_model(rng, 300, 1)
+    ref = M.ModelRef(w, 1)
+    ref.forward([42])
+    res = w["embedding"][[42]]
+    normed = M.rmsnorm(res, w["layer0.norm1"])
+    qkv = M.project(normed, w["layer0.qkv"])
+    v = qkv[:, 2304:2560]
+    att = np.concatenate([np.tile(v[:, :128], 8), np.tile(v[:, 128:], 8)], axis=1)
+    res = M.bf16(res + M.project(att, w["layer0.o"]))
+    normed = M.rmsnorm(res, w["layer0.norm2"])
+    gu = M.project(normed, w["layer0.gate_up"])
+    res = M.bf16(res + M.project(M.silu_mul(gu[:, :6144], gu[:, 6144:]), w["layer0.down"]))
+    logits = M.project(M.rmsnorm(res, w["final_norm"]), w["lm_head"])[0]
+    assert np.array_equal(ref.last_logits, logits)

@@ -85,10 +85,10 @@ def test_model_load_validation(rt, tmp_path):
     with pytest.raises(rt.McError) as e:
         rt.Model(str(tmp_path), rt.model_options(max_context_tokens=0))
     assert e.value.status == 7
-    (tmp_path / "model.wpk").write_bytes(b"x")
+    (tmp_path / "model.wpk").write_bytes(b"x")  # a package too short for its header
     with pytest.raises(rt.McError) as e:
         rt.Model(str(tmp_path), rt.model_options())
-    assert e.value.status == 7 and "weight" in str(e.value)
+    assert e.value.status == 2 and "model.wpk" in str(e.value)
 
 
 def pool_token(info, layer, pos, pt):
@@ -415,7 +415,7 @@ def test_breakdown_and_group_stats(rt, tmp_path, graphs, monkeypatch):
         assert all(x > 0.0 for x in segs[1:84:2])  # the attention segments
     L = rt._bind()
     assert L.mc_debug_breakdown_bucket_count() == 3
-    assert L.mc_debug_breakdown_bucket_name(1).startswith(b"attn")
+    assert L.mc_debug_breakdown_bucket_name(1).startswith(b"layer(attention")
     assert L.mc_debug_breakdown_bucket_of(1) == 1 and L.mc_debug_breakdown_bucket_of(84) == 2
     g = rt.BatchGroup(m, 4, 2048)
     assert g.breakdown() == -2

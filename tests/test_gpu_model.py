@@ -1,0 +1,287 @@
+"""Weight path on the GPU: the model kernels against numpy, and a whole
+model.wpk model (full geometry: 42 layers, vocabulary 130560, random weights
+shared between even and odd layers) through mc_model_load / mc_prefill /
+mc_decode_one / mc_batch_step against the forward oracle
+(oracle/model_ref.py).
+
+Tolerances: projections, norms and SwiGLU round to bf16 once, so the kernels
+are held to one bf16 ulp of the fp64 result; the 42-layer forward compares
+logits by relative L2 (< 2e-2) and cosine (> 0.999), and the greedy tokens
+where the oracle's top-2 margin leaves no doubt. Batched steps must equal solo
+decodes bit for bit (same kernels per row), and graph replay must equal eager.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import wpk_util as W
+from _util import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def P(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def stream():
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg._native.lib()
+
+
+@pytest.fixture(scope="module")
+def rt(pkg, dev):
+    import importlib
+    return importlib.import_module("minicpm5-5080fast_amd.runtime")
+
+
+def rnd_bf16(orc, rng, shape, scale=1.0):
+    return orc.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+
+
+def within_ulp(orc, got_bits, ref, ulps=1.0, frac=0.999):
+    got = orc.bf16_to_f32(got_bits).astype(np.float64)
+    err = np.abs(got - ref)
+    ok = err <= ulps * orc.bf16_ulp(ref) + 1e-30
+    return ok.mean() >= frac and np.all(err <= 2 * ulps * orc.bf16_ulp(ref) + 1e-6), \
+        (ok.mean(), err.max())
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 2048, 2048), (1, 2560, 2048), (3, 1000, 6144),
+                                   (8, 2048, 2048), (5, 777, 6144), (1, 12288, 2048)])
+def test_gemv(lib, orc, dev, M, N, K):
+    import torch
+    rng = np.random.default_rng(M * 1000 + N + K)
+    w = rnd_bf16(orc, rng, (N, K), K ** -0.5)
+    x = rnd_bf16(orc, rng, (M, K + 8))  # row stride K + 8
+    y = torch.full((M, N + 3), -1, dtype=torch.int16, device=dev)
+    dw, dx = to_dev(w, dev), to_dev(x, dev)
+    assert lib.mc_model_gemv(P(dw), P(dx), K + 8, P(y), N + 3, M, N, K, stream()) == 0
+    torch.cuda.synchronize()
+    got = from_dev(y).reshape(M, N + 3)
+    ref = orc.bf16_to_f32(x[:, :K]).astype(np.float64) @ orc.bf16_to_f32(w).astype(np.float64).T
+    ok, st = within_ulp(orc, got[:, :N], ref)
+    assert ok, st
+    assert np.all(got[:, N:] == np.uint16(0xFFFF))  # past N untouched
+
+
+@pytest.mark.parametrize("M,add,N", [(1, False, 2560), (1, True, 2560), (4, True, 12288),
+                                     (8, True, 1000)])
+def test_gemv_resnorm(lib, orc, dev, M, add, N):
+    import torch
+    from oracle import model_ref as R
+    rng = np.random.default_rng(M + N)
+    w = rnd_bf16(orc, rng, (N, 2048), 2048 ** -0.5)
+    res = rnd_bf16(orc, rng, (M, 2048), 2.0)
+    dlt = rnd_bf16(orc, rng, (M, 2048), 0.5)
+    g = orc.f32_to_bf16(1 + 0.1 * rng.standard_normal(2048, dtype=np.float32))
+    dres, ddl, dg, dw = (to_dev(a, dev) for a in (res, dlt, g, w))
+    rout = torch.zeros(M * 2048, dtype=torch.int16, device=dev)
+    y = torch.zeros(M * N, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemv_resnorm(P(dw), P(dres), P(ddl) if add else None, P(dg),
+                                     P(rout) if add else None, 2048, P(y), N, M, N,
+                                     C.c_float(1e-6), stream()) == 0
+    torch.cuda.synchronize()
+    r = orc.bf16_to_f32(res) + (orc.bf16_to_f32(dlt) if add else 0)
+    r = R.bf16(r)
+    if add:
+        assert np.array_equal(from_dev(rout).reshape(M, 2048), orc.f32_to_bf16(r))
+    x = R.rmsnorm(r, orc.bf16_to_f32(g))
+    ref = x.astype(np.float64) @ orc.bf16_to_f32(w).astype(np.float64).T
+    ok, st = within_ulp(orc, from_dev(y).reshape(M, N), ref, ulps=2.0, frac=0.99)
+    assert ok, st
+
+
+@pytest.mark.parametrize("M,K", [(1, 6144), (2, 6144), (3, 2048)])
+def test_gemv_swiglu(lib, orc, dev, M, K):
+    import torch
+    from oracle import model_ref as R
+    rng = np.random.default_rng(M + K)
+    N = 2048
+    w = rnd_bf16(orc, rng, (N, K), K ** -0.5)
+    gu = rnd_bf16(orc, rng, (M, 2 * K), 2.0)
+    y = torch.zeros(M * N, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemv_swiglu(P(to_dev(w, dev)), P(to_dev(gu, dev)), 2 * K, P(y), N, M, N,
+                                    K, stream()) == 0
+    torch.cuda.synchronize()
+    g = orc.bf16_to_f32(gu)
+    x = R.silu_mul(g[:, :K], g[:, K:])
+    ref = x.astype(np.float64) @ orc.bf16_to_f32(w).astype(np.float64).T
+    ok, st = within_ulp(orc, from_dev(y).reshape(M, N), ref, ulps=2.0, frac=0.99)
+    assert ok, st
+
+
+def test_norm_swiglu_embedding_rows(lib, orc, dev):
+    import torch
+    from oracle import model_ref as R
+    rng = np.random.default_rng(11)
+    rows = 37
+    res = rnd_bf16(orc, rng, (rows, 2048), 3.0)
+    dlt = rnd_bf16(orc, rng, (rows, 2048))
+    g = orc.f32_to_bf16(1 + 0.1 * rng.standard_normal(2048, dtype=np.float32))
+    dres, out = to_dev(res, dev), torch.zeros(rows * 2048, dtype=torch.int16, device=dev)
+    assert lib.mc_model_rmsnorm_rows(P(dres), P(to_dev(dlt, dev)), P(to_dev(g, dev)), P(out), rows,
+                                     2048, C.c_float(1e-6), stream()) == 0
+    torch.cuda.synchronize()
+    r = R.bf16(orc.bf16_to_f32(res) + orc.bf16_to_f32(dlt))
+    assert np.array_equal(from_dev(dres).reshape(rows, 2048), orc.f32_to_bf16(r))
+    ref = R.rmsnorm(r, orc.bf16_to_f32(g)).astype(np.float64)
+    got = orc.bf16_to_f32(from_dev(out)).reshape(rows, 2048)
+    assert np.mean(got == ref) > 0.99 and np.all(np.abs(got - ref) <= orc.bf16_ulp(ref) + 1e-30)
+    # SwiGLU rows
+    src = rnd_bf16(orc, rng, (rows, 2 * 6144), 3.0)
+    sw = torch.zeros(rows * 6144, dtype=torch.int16, device=dev)
+    assert lib.mc_model_swiglu_rows(P(to_dev(src, dev)), P(sw), rows, 6144, stream()) == 0
+    torch.cuda.synchronize()
+    s = orc.bf16_to_f32(src)
+    ref = R.silu_mul(s[:, :6144], s[:, 6144:])
+    got = orc.bf16_to_f32(from_dev(sw)).reshape(rows, 6144)
+    assert np.mean(got == ref) > 0.99 and np.all(np.abs(got - ref) <= orc.bf16_ulp(ref) + 1e-30)
+    # embedding (direct ids and per-slot token pointers): exact rows
+    table = rnd_bf16(orc, rng, (500, 2048))
+    ids = np.array([5, 0, 499, 5, 17], dtype=np.int32)
+    dt = to_dev(table, dev)
+    e1 = torch.zeros(5 * 2048, dtype=torch.int16, device=dev)
+    assert lib.mc_model_embedding_gather(P(dt), P(to_dev(ids, dev)), None, P(e1), 2048, 5,
+                                         stream()) == 0
+    toks = [torch.tensor([int(i)], dtype=torch.int32, device=dev) for i in ids]
+    tab = torch.tensor([t.data_ptr() for t in toks], dtype=torch.int64, device=dev)
+    e2 = torch.zeros(5 * 2048, dtype=torch.int16, device=dev)
+    assert lib.mc_model_embedding_gather(P(dt), None, P(tab), P(e2), 2048, 5, stream()) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(e1).reshape(5, 2048), table[ids])
+    assert np.array_equal(from_dev(e2).reshape(5, 2048), table[ids])
+
+
+def test_argmax(lib, orc, dev):
+    import torch
+    rng = np.random.default_rng(13)
+    n = 130560
+    lg = rnd_bf16(orc, rng, (3, n))
+    lg[1, 70000] = lg[1, 1234] = orc.f32_to_bf16(np.float32([100.0]))[0]  # tie: lowest index
+    lg[2, n - 1] = orc.f32_to_bf16(np.float32([50.0]))[0]
+    out = torch.full((3,), -1, dtype=torch.int32, device=dev)
+    assert lib.mc_model_argmax_bf16(P(to_dev(lg, dev)), n, 3, P(out), None, stream()) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert got[0] == int(np.argmax(orc.bf16_to_f32(lg[0])))
+    assert got[1] == 1234 and got[2] == n - 1
+
+
+# ---------------- whole model through the mc_* ABI ----------------
+
+@pytest.fixture(scope="module")
+def model_dir(tmp_path_factory, orc):
+    """A full-geometry model.wpk with random weights (two layer sets)."""
+    d = tmp_path_factory.mktemp("wpk")
+    secs = W.model_sections(2)
+    blobs = W.random_blobs(1234, 2, scale=1.0)
+    W.write_wpk(os.path.join(d, "model.wpk"), secs, blobs)
+    return str(d), W.weights_f32(secs, blobs)
+
+
+def compare_logits(got, ref):
+    d = got.astype(np.float64) - ref.astype(np.float64)
+    rel = np.linalg.norm(d) / np.linalg.norm(ref)
+    cos = float(got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref)))
+    return rel, cos
+
+
+def clear_winner(logits):
+    top = np.sort(logits)[-2:]
+    return top[1] - top[0] > 0.05 * np.std(logits)
+
+
+def test_model_prefill_decode_vs_oracle(rt, orc, model_dir):
+    from oracle import model_ref as R
+    path, w = model_dir
+    m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2))
+    s = rt.Session(m)
+    ref = R.ModelRef(w, 42)
+    prompt = [1, 500, 130559, 77, 9, 12345, 3, 3, 42]
+    s.prefill(prompt)
+    ref.forward(prompt)
+    rel, cos = compare_logits(s.last_logits(), ref.last_logits)
+    print("prefill logits rel", rel, "cos", cos)
+    assert rel < 2e-2 and cos > 0.999
+    cfg = rt.gen_config(max_new_tokens=16)
+    for step in range(4):
+        tok = s.decode_one(cfg)
+        want = ref.next_token
+        if clear_winner(ref.last_logits):
+            assert tok == want, (step, tok, want)
+        ref.next_token = tok  # both continue from the GPU's token
+        ref.decode()
+        rel, cos = compare_logits(s.last_logits(), ref.last_logits)
+        print("decode", step, "token", tok, "rel", rel, "cos", cos)
+        assert rel < 2e-2 and cos > 0.999
+    info = s.info()
+    assert info["seq_len"] == len(prompt) + 4
+    seq = s.seq(len(prompt) + 4)
+    assert seq[:len(prompt)] == prompt
+    s.close()
+    m.close()
+
+
+def test_model_graph_equals_eager_and_batch_equals_solo(rt, model_dir):
+    """Greedy tokens and logits: graph replay == eager, and a batch step of two
+    sessions == their solo decodes (bitwise)."""
+    path, _ = model_dir
+    prompts = [[5, 6, 7, 8, 9, 10, 11], [200, 300, 400]]
+    cfg = rt.gen_config(max_new_tokens=16)
+    runs = {}
+    for graphs in (0, 1):
+        m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2,
+                                            enable_cuda_graph=graphs))
+        toks, lg = [], []
+        for p in prompts:
+            s = rt.Session(m)
+            s.prefill(p)
+            t = [s.decode_one(cfg) for _ in range(3)]
+            toks.append(t)
+            lg.append(s.last_logits())
+            s.close()
+        runs[graphs] = (toks, lg)
+        # batch: both prompts in one group
+        ss = [rt.Session(m) for _ in prompts]
+        for s, p in zip(ss, prompts):
+            s.prefill(p)
+        g = rt.BatchGroup(m, 2, 4096)
+        slots = [g.add(s) for s in ss]
+        bt = [g.step(slots, [cfg, cfg]) for _ in range(3)]
+        assert [list(x) for x in zip(*bt)] == toks, (bt, toks)
+        for i, sl in enumerate(slots):
+            assert np.array_equal(g.last_logits(sl), lg[i])
+        g.close()
+        for s in ss:
+            s.close()
+        m.close()
+    assert runs[0][0] == runs[1][0]
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert np.array_equal(a, b)
+
+
+def test_model_rejects_sampling_and_bad_package(rt, model_dir, tmp_path):
+    path, _ = model_dir
+    m = rt.Model(path, rt.model_options(max_context_tokens=1024, max_sessions=1))
+    s = rt.Session(m)
+    s.prefill([1, 2, 3])
+    with pytest.raises(rt.McError) as e:
+        s.decode_one(rt.gen_config(temperature=0.8, top_k=40))
+    assert e.value.status == 7
+    assert s.decode_one(rt.gen_config()) >= 0  # greedy still fine
+    s.close()
+    m.close()
+    bad = tmp_path / "bad"
+    bad.mkdir()
+    (bad / "model.wpk").write_bytes(b"MKP0" + b"\x00" * 60)
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(bad), rt.model_options())
+    assert e.value.status == 4
