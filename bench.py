@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c4,c3,c1,c2,c5,pf,alloc")
+    ap.add_argument("--configs", default="c4,c3,c1,c2,c5,pf,alloc,model")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="no HIP graphs (eager launches)")
@@ -525,6 +525,73 @@ def cpu_baseline(seconds: float):
     }
 
 
+def bench_model(pkg, torch, steps):
+    """Whole-model greedy decoding with weights: a full-geometry model.wpk of
+    random bf16 weights (even / odd layers share one weight set, embedding
+    and lm_head one table; the device holds every section separately, 5.03 GB)
+    loaded through mc_model_load with HIP graphs; solo decode after a
+    2048-token prompt and 8-session batch steps. Each decode streams every
+    layer weight and the lm_head once: 4.50 GB per step."""
+    import importlib
+    import shutil
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    W = importlib.import_module("wpk_util")
+    rt = importlib.import_module("minicpm5-5080fast_amd.runtime")
+    d = tempfile.mkdtemp(prefix="mc_wpk_")
+    try:
+        secs = W.model_sections(2)
+        W.write_wpk(os.path.join(d, "model.wpk"), secs, W.random_blobs(7, 2))
+        t0 = time.perf_counter()
+        m = rt.Model(d, rt.model_options(max_context_tokens=8192, max_sessions=9,
+                                         enable_cuda_graph=1))
+        load_s = time.perf_counter() - t0
+        weight_bytes = (W.LAYERS * (W.QKV * W.HIDDEN + W.HIDDEN * W.HIDDEN
+                                    + 2 * W.INTER * W.HIDDEN + W.HIDDEN * W.INTER)
+                        + W.VOCAB * W.HIDDEN) * 2
+        cfg = rt.gen_config(max_new_tokens=1 << 20)
+        prompt = [(i * 7919) % W.VOCAB for i in range(2048)]
+        s = rt.Session(m)
+        s.prefill(prompt)  # first use: rocBLAS loads its GEMM kernels
+        s.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        s.prefill(prompt)
+        prefill_s = time.perf_counter() - t0
+        for _ in range(3):
+            s.decode_one(cfg)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            s.decode_one(cfg)
+        solo = (time.perf_counter() - t0) / steps
+        ss = [rt.Session(m) for _ in range(8)]
+        for i, x in enumerate(ss):
+            x.prefill(prompt[:512 + 64 * i])
+        g = rt.BatchGroup(m, 8, 8192)
+        slots = [g.add(x) for x in ss]
+        for _ in range(3):
+            g.step(slots, [cfg] * 8)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.step(slots, [cfg] * 8)
+        batch = (time.perf_counter() - t0) / steps
+        g.close()
+        for x in ss + [s]:
+            x.close()
+        m.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return {
+        "weights": "random bf16, full MiniCPM5-2B geometry (42 layers, vocab 130560)",
+        "load_s": load_s, "weight_bytes_per_step": weight_bytes,
+        "prefill_2048_ms": prefill_s * 1e3, "prefill_tokens_per_s": 2048 / prefill_s,
+        "decode_ms_per_token": solo * 1e3, "decode_tokens_per_s": 1.0 / solo,
+        "decode_weight_gbs": weight_bytes / solo / 1e9,
+        "decode_pct_hbm_peak": 100.0 * weight_bytes / solo / 1e9 / HBM_PEAK_GBS,
+        "batch8_ms_per_step": batch * 1e3, "batch8_tokens_per_s": 8.0 / batch,
+    }
+
+
 def bench_alloc(kvm):
     """Host page allocator (reference kv_cache.cpp:8-91 semantics, shared-pool
     form): 8 sessions grown to 131072 tokens of 64-token pages in one pool,
@@ -605,6 +672,11 @@ def main():
     if "alloc" in cfgs:
         res["alloc_host"] = bench_alloc(kvm)
         log(res["alloc_host"])
+    if "model" in cfgs:
+        log("whole model with weights: decode, batch 8, prefill ...")
+        res["model_decode"] = bench_model(pkg, torch, max(8, args.steps))
+        log(res["model_decode"])
+        torch.cuda.empty_cache()
     if "pf" in cfgs:
         for base in (0, 8448):
             log(f"prefill attention 8448 tokens at base {base} ...")

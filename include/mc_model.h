@@ -70,6 +70,19 @@ mc_status_t mc_model_gemv_resnorm(const uint16_t* d_w, const uint16_t* d_res_in,
                                   uint16_t* d_res_out, uint32_t ldr, uint16_t* d_y, uint32_t ldy,
                                   uint32_t M, uint32_t N, float eps, void* stream);
 
+/* launch_gemv_rows_prologue (kernels.h:743) followed by launch_swiglu_gated
+ * (kernels.h:589) in one launch: with the prologue of
+ * mc_model_gemv_resnorm, output column i < I of row m is
+ * bf16(silu(g) * u) where g = bf16(d_w[i] . x_m) and u = bf16(d_w[I + i] . x_m)
+ * (d_w: the gate_up matrix [2I][2048], gate rows then up rows), i.e. the
+ * gate_up projection rounded to bf16 and then the SwiGLU, without writing
+ * the projection. d_y rows hold I values (stride ldy). */
+mc_status_t mc_model_gemv_resnorm_swiglu(const uint16_t* d_w, const uint16_t* d_res_in,
+                                         const uint16_t* d_add, const uint16_t* d_norm_w,
+                                         uint16_t* d_res_out, uint32_t ldr, uint16_t* d_y,
+                                         uint32_t ldy, uint32_t M, uint32_t I, float eps,
+                                         void* stream);
+
 /* launch_gemv_rows_swiglu (kernels.h:760), for M <= 8 rows: x =
  * swiglu(d_gate_up rows [M][ldx], gate in columns 0..K-1, up in K..2K-1) as
  * mc_model_swiglu_rows, then d_y = GEMV(d_w, x). K is 2048 or 6144. */
@@ -80,9 +93,15 @@ mc_status_t mc_model_gemv_swiglu(const uint16_t* d_w, const uint16_t* d_gate_up,
 /* launch_sampling_greedy_bf16 (kernels.h:610) for rows == 1 and
  * launch_batch_argmax_bf16 (kernels.h:641): per row of n bf16 logits the
  * index of the largest value compared in fp32, ties to the lowest index,
- * written to d_out[r] or to *d_slot_tok[r]. Exactly one of the two. */
+ * written to d_out[r] or to *d_slot_tok[r]. Exactly one of the two. With
+ * stage buffers (MC_MODEL_ARGMAX_SLICES floats / ints per row, as the
+ * reference's d_stage_v / d_stage_i) the row is scanned by that many
+ * workgroups and the slices reduced by a second launch; with NULL one
+ * workgroup scans the row. */
+#define MC_MODEL_ARGMAX_SLICES 64u
 mc_status_t mc_model_argmax_bf16(const uint16_t* d_logits, uint32_t n, uint32_t rows,
-                                 int32_t* d_out, int32_t* const* d_slot_tok, void* stream);
+                                 int32_t* d_out, int32_t* const* d_slot_tok, float* d_stage_v,
+                                 int32_t* d_stage_i, void* stream);
 
 /* WeightLoader::load_wpk's checks (weight_loader.h:120-137,
  * weight_loader.cpp:201-360) without a device: reads the model.wpk at

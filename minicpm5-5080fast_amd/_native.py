@@ -88,7 +88,9 @@ _SIGS = {
     "mc_model_gemv_resnorm": (C.c_int, [_P, _P, _P, _P, _P, _u32, _P, _u32, _u32, _u32,
                                         C.c_float, _P]),
     "mc_model_gemv_swiglu": (C.c_int, [_P, _P, _u32, _P, _u32, _u32, _u32, _u32, _P]),
-    "mc_model_argmax_bf16": (C.c_int, [_P, _u32, _u32, _P, _P, _P]),
+    "mc_model_gemv_resnorm_swiglu": (C.c_int, [_P, _P, _P, _P, _P, _u32, _P, _u32, _u32, _u32,
+                                               C.c_float, _P]),
+    "mc_model_argmax_bf16": (C.c_int, [_P, _u32, _u32, _P, _P, _P, _P, _P]),
     "mc_model_wpk_check": (C.c_int, [C.c_char_p, C.POINTER(C.c_uint64)]),
 }
 

@@ -18,8 +18,10 @@
 //   * decode (one row) and batch steps (n <= 8 rows): every projection is the
 //     HBM-streaming GEMV of model_kernels.hip, with the residual add + RMSNorm
 //     fused into the GEMV that consumes it (qkv, gate_up, lm_head) and the
-//     SwiGLU fused into the down projection (the reference's fused decode
-//     chain, forward.cpp:165-190); the residual alternates between two
+//     SwiGLU fused into the gate_up projection's output (each output column
+//     streams its gate and up rows together; the reference fuses it into the
+//     down projection's input, forward.cpp:165-190, which would repeat the
+//     SwiGLU in every workgroup); the residual alternates between two
 //     buffers so that the workgroup writing the new residual never races the
 //     workgroups still reading the old one. Attention is the phase0 decode
 //     (RoPE + K/V append + split-KV attention in one chunk kernel).
@@ -82,7 +84,8 @@ size_t forward_act_bytes(uint32_t rows, uint32_t logit_rows) {
            + a256(r * 2u * kInter * 2u)     // gate_up
            + a256(r * kInter * 2u)          // mlp
            + a256(r * kHidden * 2u)         // down
-           + a256((size_t)logit_rows * kVocabSize * 2u);
+           + a256((size_t)logit_rows * kVocabSize * 2u)
+           + a256((size_t)logit_rows * MC_MODEL_ARGMAX_SLICES * 4u) * 2u;  // argmax stages
 }
 
 void forward_carve(Forward& f, char* p, uint32_t rows, uint32_t logit_rows) {
@@ -102,6 +105,8 @@ void forward_carve(Forward& f, char* p, uint32_t rows, uint32_t logit_rows) {
     f.mlp = take(r * kInter * 2u);
     f.down = take(r * kHidden * 2u);
     f.logits = take((size_t)logit_rows * kVocabSize * 2u);
+    f.stage_v = reinterpret_cast<float*>(take((size_t)logit_rows * MC_MODEL_ARGMAX_SLICES * 4u));
+    f.stage_i = reinterpret_cast<int32_t*>(take((size_t)logit_rows * MC_MODEL_ARGMAX_SLICES * 4u));
     f.rows = rows;
 }
 
@@ -135,7 +140,8 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
     }
     FWD_OR_RETURN(mc_model_gemv(w.lm_head, f.normed + (size_t)(n - 1u) * kHidden, kHidden,
                                 f.logits, kVocabSize, 1, kVocabSize, kHidden, st));
-    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, st);
+    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v, f.stage_i,
+                                st);
 }
 
 mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_next,
@@ -161,17 +167,19 @@ mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_ne
                                              f.chunk_pos, f.partials2));
         FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn, kHidden, f.o_out, kHidden, 1, kHidden, kHidden,
                                     st));
-        FWD_OR_RETURN(mc_model_gemv_resnorm(w.gate_up[l], cur, f.o_out, w.norm2[l], other, kHidden,
-                                            f.gate_up, 2u * kInter, 1, 2u * kInter, kRmsEps, st));
+        FWD_OR_RETURN(mc_model_gemv_resnorm_swiglu(w.gate_up[l], cur, f.o_out, w.norm2[l], other,
+                                                   kHidden, f.mlp, kInter, 1, kInter, kRmsEps,
+                                                   st));
         std::swap(cur, other);
-        FWD_OR_RETURN(mc_model_gemv_swiglu(w.down[l], f.gate_up, 2u * kInter, f.down, kHidden, 1,
-                                           kHidden, kInter, st));
+        FWD_OR_RETURN(mc_model_gemv(w.down[l], f.mlp, kInter, f.down, kHidden, 1, kHidden, kInter,
+                                    st));
         pending = f.down;
         mark();
     }
     FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur, pending, w.final_norm, nullptr, kHidden,
                                         f.logits, kVocabSize, 1, kVocabSize, kRmsEps, st));
-    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, st);
+    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v, f.stage_i,
+                                st);
 }
 
 mc_status_t forward_batch(const Forward& f, const BatchKv& b, const Marker& mark) {
@@ -199,17 +207,19 @@ mc_status_t forward_batch(const Forward& f, const BatchKv& b, const Marker& mark
                                                    f.partials2));
         FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn, kHidden, f.o_out, kHidden, n, kHidden, kHidden,
                                     st));
-        FWD_OR_RETURN(mc_model_gemv_resnorm(w.gate_up[l], cur, f.o_out, w.norm2[l], other, kHidden,
-                                            f.gate_up, 2u * kInter, n, 2u * kInter, kRmsEps, st));
+        FWD_OR_RETURN(mc_model_gemv_resnorm_swiglu(w.gate_up[l], cur, f.o_out, w.norm2[l], other,
+                                                   kHidden, f.mlp, kInter, n, kInter, kRmsEps,
+                                                   st));
         std::swap(cur, other);
-        FWD_OR_RETURN(mc_model_gemv_swiglu(w.down[l], f.gate_up, 2u * kInter, f.down, kHidden, n,
-                                           kHidden, kInter, st));
+        FWD_OR_RETURN(mc_model_gemv(w.down[l], f.mlp, kInter, f.down, kHidden, n, kHidden, kInter,
+                                    st));
         pending = f.down;
         mark();
     }
     FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur, pending, w.final_norm, nullptr, kHidden,
                                         f.logits, kVocabSize, n, kVocabSize, kRmsEps, st));
-    return mc_model_argmax_bf16(f.logits, kVocabSize, n, nullptr, b.d_slot_tok, st);
+    return mc_model_argmax_bf16(f.logits, kVocabSize, n, nullptr, b.d_slot_tok, f.stage_v,
+                                f.stage_i, st);
 }
 
 }  // namespace mckv

@@ -64,6 +64,8 @@ struct Forward {
     uint16_t *res_a = nullptr, *res_b = nullptr, *normed = nullptr, *qkv = nullptr,
              *attn = nullptr, *o_out = nullptr, *gate_up = nullptr, *mlp = nullptr,
              *down = nullptr, *logits = nullptr;
+    float* stage_v = nullptr;    // argmax slice results
+    int32_t* stage_i = nullptr;
     uint32_t rows = 0;
 };
 

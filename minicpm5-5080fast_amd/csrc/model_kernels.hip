@@ -40,7 +40,12 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kMaxRows = MC_MODEL_GEMV_MAX_ROWS;  // activation rows per GEMV
-constexpr uint32_t kMaxBlocks = 2048;                   // 8 workgroups per CU
+// GEMV grid: at most 512 workgroups (2 per CU on 256 CUs; 256 when the
+// staged activations need more than 64 KB of LDS), so every workgroup stages
+// its activation rows (and runs the norm prologue) once and then streams
+// rows; more workgroups only repeat the staging (measured: 2048 workgroups
+// made the 8-row gate_up projection 4x slower).
+constexpr uint32_t kMaxBlocks = 512;
 
 __device__ __forceinline__ uint4 ld_stream(const uint16_t* p) {
     return __builtin_bit_cast(uint4,
@@ -183,44 +188,58 @@ struct GemvArgs {
 
 // K = 512 * KC (16-byte chunks per lane per row). kProResnorm needs K = 2048
 // (one chunk per thread and row).
-template <uint32_t M, uint32_t PRO, uint32_t KC>
+// SWI: SwiGLU epilogue. Output column n (n < a.N) takes the weight rows n
+// (gate) and a.N + n (up) of a [2 a.N][K] matrix: y = bf16(silu(g) * u) with
+// g, u the two dot products rounded to bf16 first (the projection's output
+// rounding), as a gate_up projection followed by the SwiGLU kernel.
+template <uint32_t M, uint32_t PRO, uint32_t KC, bool SWI = false>
 __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvArgs a) {
     constexpr uint32_t K = 512u * KC, NCH = K / 8u;
     static_assert(PRO != kProResnorm || K == 2048u, "the norm prologue covers 2048 dims");
     __shared__ uint4 sx[M * NCH];
-    __shared__ float s4[4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     // Stage the activation rows (after the prologue) into LDS.
     if constexpr (PRO == kProResnorm) {
+        // all M rows' sums of squares in one workgroup reduction
+        __shared__ float s_part[M][4];
+        uint4 v[M];
+        float ss[M];
 #pragma unroll
         for (uint32_t m = 0; m < M; ++m) {
-            uint4 v = ld16(a.res_in + (size_t)m * a.ldr + 8u * tid);
+            v[m] = ld16(a.res_in + (size_t)m * a.ldr + 8u * tid);
             if (a.addend != nullptr) {
                 const uint4 d = ld16(a.addend + (size_t)m * a.ldr + 8u * tid);
-                v.x = pack2(lo_f(v.x) + lo_f(d.x), hi_f(v.x) + hi_f(d.x));
-                v.y = pack2(lo_f(v.y) + lo_f(d.y), hi_f(v.y) + hi_f(d.y));
-                v.z = pack2(lo_f(v.z) + lo_f(d.z), hi_f(v.z) + hi_f(d.z));
-                v.w = pack2(lo_f(v.w) + lo_f(d.w), hi_f(v.w) + hi_f(d.w));
+                v[m].x = pack2(lo_f(v[m].x) + lo_f(d.x), hi_f(v[m].x) + hi_f(d.x));
+                v[m].y = pack2(lo_f(v[m].y) + lo_f(d.y), hi_f(v[m].y) + hi_f(d.y));
+                v[m].z = pack2(lo_f(v[m].z) + lo_f(d.z), hi_f(v[m].z) + hi_f(d.z));
+                v[m].w = pack2(lo_f(v[m].w) + lo_f(d.w), hi_f(v[m].w) + hi_f(d.w));
             }
             if (a.res_out != nullptr && blockIdx.x == 0u)
-                *reinterpret_cast<uint4*>(a.res_out + (size_t)m * a.ldr + 8u * tid) = v;
-            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-            float ss = 0.f;
+                *reinterpret_cast<uint4*>(a.res_out + (size_t)m * a.ldr + 8u * tid) = v[m];
+            const uint32_t u[4] = {v[m].x, v[m].y, v[m].z, v[m].w};
+            float t = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float p = lo_f(u[i]), q = hi_f(u[i]);
-                ss = fmaf(p, p, ss);
-                ss = fmaf(q, q, ss);
+                t = fmaf(p, p, t);
+                t = fmaf(q, q, t);
             }
-            const float inv = 1.0f / sqrtf(block_sum(ss, s4) / (float)K + a.eps);
-            const uint4 g = ld16(a.norm_w + 8u * tid);
+            ss[m] = wave_sum(t);
+            if (lane == 0u) s_part[m][wave] = ss[m];
+        }
+        __syncthreads();
+        const uint4 g = ld16(a.norm_w + 8u * tid);
+#pragma unroll
+        for (uint32_t m = 0; m < M; ++m) {
+            const float tot = ((s_part[m][0] + s_part[m][1]) + s_part[m][2]) + s_part[m][3];
+            const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
             uint4 o;
-            o.x = pack2(lo_f(v.x) * inv * lo_f(g.x), hi_f(v.x) * inv * hi_f(g.x));
-            o.y = pack2(lo_f(v.y) * inv * lo_f(g.y), hi_f(v.y) * inv * hi_f(g.y));
-            o.z = pack2(lo_f(v.z) * inv * lo_f(g.z), hi_f(v.z) * inv * hi_f(g.z));
-            o.w = pack2(lo_f(v.w) * inv * lo_f(g.w), hi_f(v.w) * inv * hi_f(g.w));
+            o.x = pack2(lo_f(v[m].x) * inv * lo_f(g.x), hi_f(v[m].x) * inv * hi_f(g.x));
+            o.y = pack2(lo_f(v[m].y) * inv * lo_f(g.y), hi_f(v[m].y) * inv * hi_f(g.y));
+            o.z = pack2(lo_f(v[m].z) * inv * lo_f(g.z), hi_f(v[m].z) * inv * hi_f(g.z));
+            o.w = pack2(lo_f(v[m].w) * inv * lo_f(g.w), hi_f(v[m].w) * inv * hi_f(g.w));
             sx[m * NCH + tid] = o;
         }
     } else {
@@ -233,51 +252,87 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvArgs a) {
     }
     __syncthreads();
 
+    // The row is streamed in groups of kG chunks per lane (K / (512 kG) groups
+    // per row); the next group's loads (of this row or the next one) are
+    // issued before the current group is multiplied, so each lane keeps 2 kG
+    // 16-byte loads in flight whatever K is.
+    constexpr uint32_t kG = 4u, NG = KC / kG;
+    constexpr uint32_t R = SWI ? 2u : 1u;  // weight rows per output column
+    static_assert(KC % kG == 0u, "whole chunk groups");
     const uint32_t stride = gridDim.x * 4u;
-    uint32_t n = blockIdx.x * 4u + wave;
+    uint32_t n = blockIdx.x * 4u + wave, g = 0u;
     if (n >= a.N) return;  // wave-uniform; no barrier follows
-    uint4 wc[KC];
+    auto load = [&](uint4 (&dst)[R][kG], uint32_t col, uint32_t grp) {
 #pragma unroll
-    for (uint32_t c = 0; c < KC; ++c) wc[c] = ld_stream(a.w + (size_t)n * K + 8u * (lane + 64u * c));
+        for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+            for (uint32_t c = 0; c < kG; ++c)
+                dst[r][c] = ld_stream(a.w + (size_t)(col + r * a.N) * K +
+                                      8u * (lane + 64u * (grp * kG + c)));
+    };
+    uint4 wc[R][kG];
+    load(wc, n, g);
+    float acc[R][M];
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+        for (uint32_t m = 0; m < M; ++m) acc[r][m] = 0.f;
     while (true) {
-        const uint32_t n2 = n + stride;
-        const bool more = n2 < a.N;
-        uint4 wn[KC];
-        if (more) {
-#pragma unroll
-            for (uint32_t c = 0; c < KC; ++c)
-                wn[c] = ld_stream(a.w + (size_t)n2 * K + 8u * (lane + 64u * c));
+        uint32_t g2 = g + 1u, n2 = n;
+        if (g2 == NG) {
+            g2 = 0u;
+            n2 = n + stride;
         }
-        float acc[M];
+        const bool more = n2 < a.N;
+        uint4 wn[R][kG];
+        if (more) load(wn, n2, g2);
 #pragma unroll
-        for (uint32_t m = 0; m < M; ++m) acc[m] = 0.f;
-#pragma unroll
-        for (uint32_t c = 0; c < KC; ++c) {
-            const uint4 wv = wc[c];
+        for (uint32_t c = 0; c < kG; ++c) {
+            const uint32_t ch = lane + 64u * (g * kG + c);
 #pragma unroll
             for (uint32_t m = 0; m < M; ++m) {
-                const uint4 xv = sx[m * NCH + lane + 64u * c];
-                float t = acc[m];
-                t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.x),
-                                                    __builtin_bit_cast(bf16x2_t, xv.x), t, false);
-                t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.y),
-                                                    __builtin_bit_cast(bf16x2_t, xv.y), t, false);
-                t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.z),
-                                                    __builtin_bit_cast(bf16x2_t, xv.z), t, false);
-                t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.w),
-                                                    __builtin_bit_cast(bf16x2_t, xv.w), t, false);
-                acc[m] = t;
+                const uint4 xv = sx[m * NCH + ch];
+#pragma unroll
+                for (uint32_t r = 0; r < R; ++r) {
+                    const uint4 wv = wc[r][c];
+                    float t = acc[r][m];
+                    t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.x),
+                                                        __builtin_bit_cast(bf16x2_t, xv.x), t,
+                                                        false);
+                    t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.y),
+                                                        __builtin_bit_cast(bf16x2_t, xv.y), t,
+                                                        false);
+                    t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.z),
+                                                        __builtin_bit_cast(bf16x2_t, xv.z), t,
+                                                        false);
+                    t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.w),
+                                                        __builtin_bit_cast(bf16x2_t, xv.w), t,
+                                                        false);
+                    acc[r][m] = t;
+                }
             }
         }
+        if (g == NG - 1u) {  // column complete (wave-uniform)
 #pragma unroll
-        for (uint32_t m = 0; m < M; ++m) {
-            const float s = wave_sum(acc[m]);
-            if (lane == m) a.y[(size_t)m * a.ldy + n] = f32_to_bf16(s);
+            for (uint32_t m = 0; m < M; ++m) {
+                float v = wave_sum(acc[0][m]);
+                if constexpr (SWI) {
+                    const float gt = bf16_to_f32(f32_to_bf16(v));
+                    const float up = bf16_to_f32(f32_to_bf16(wave_sum(acc[1][m])));
+                    v = silu_mul(gt, up);
+                }
+                if (lane == m) a.y[(size_t)m * a.ldy + n] = f32_to_bf16(v);
+#pragma unroll
+                for (uint32_t r = 0; r < R; ++r) acc[r][m] = 0.f;
+            }
         }
         if (!more) break;
 #pragma unroll
-        for (uint32_t c = 0; c < KC; ++c) wc[c] = wn[c];
+        for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+            for (uint32_t c = 0; c < kG; ++c) wc[r][c] = wn[r][c];
         n = n2;
+        g = g2;
     }
 }
 
@@ -289,6 +344,57 @@ __device__ __forceinline__ void better(float& bv, uint32_t& bi, float v, uint32_
         bi = i;
     }
 }
+// Stage 1 of the two-stage argmax: grid = (kArgSlices, rows), block 256;
+// block s scans slice s of the row and writes its (value, index).
+constexpr uint32_t kArgSlices = 64;
+__global__ void __launch_bounds__(256)
+    argmax_slices_kernel(const uint16_t* __restrict__ logits, uint32_t n,
+                         float* __restrict__ stage_v, int32_t* __restrict__ stage_i) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const uint16_t* l = logits + (size_t)blockIdx.y * n;
+    const uint32_t per = (n + kArgSlices - 1u) / kArgSlices;
+    const uint32_t lo = blockIdx.x * per, hi = min(lo + per, n);
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t i = lo + threadIdx.x; i < hi; i += 256u) better(bv, bi, bf16_to_f32(l[i]), i);
+#pragma unroll
+    for (uint32_t off = 1; off < 64u; off <<= 1) {
+        const float ov = __shfl_xor(bv, (int)off);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, (int)off);
+        better(bv, bi, ov, oi);
+    }
+    if ((threadIdx.x & 63u) == 0u) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0u) {
+        for (uint32_t w = 1; w < 4u; ++w) better(bv, bi, sv[w], si[w]);
+        stage_v[blockIdx.y * kArgSlices + blockIdx.x] = bv;
+        stage_i[blockIdx.y * kArgSlices + blockIdx.x] = (int32_t)bi;
+    }
+}
+
+// Stage 2: grid = rows, block 64 (one slice result per lane).
+__global__ void __launch_bounds__(64)
+    argmax_final_kernel(const float* __restrict__ stage_v, const int32_t* __restrict__ stage_i,
+                        int32_t* out_tok, int32_t* const* __restrict__ slot_tok) {
+    float bv = stage_v[blockIdx.x * kArgSlices + threadIdx.x];
+    uint32_t bi = (uint32_t)stage_i[blockIdx.x * kArgSlices + threadIdx.x];
+#pragma unroll
+    for (uint32_t off = 1; off < 64u; off <<= 1) {
+        const float ov = __shfl_xor(bv, (int)off);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, (int)off);
+        better(bv, bi, ov, oi);
+    }
+    if (threadIdx.x == 0u) {
+        const int32_t tok = bi == 0xFFFFFFFFu ? 0 : (int32_t)bi;
+        if (slot_tok != nullptr) *slot_tok[blockIdx.x] = tok;
+        else out_tok[blockIdx.x] = tok;
+    }
+}
+
 __global__ void __launch_bounds__(1024)
     argmax_kernel(const uint16_t* __restrict__ logits, uint32_t n, int32_t* out_tok,
                   int32_t* const* __restrict__ slot_tok) {
@@ -319,24 +425,25 @@ __global__ void __launch_bounds__(1024)
     }
 }
 
-template <uint32_t M, uint32_t PRO, uint32_t KC>
+template <uint32_t M, uint32_t PRO, uint32_t KC, bool SWI>
 void launch_gemv_t(const GemvArgs& a, hipStream_t st) {
     uint32_t blocks = (a.N + 3u) / 4u;
-    if (blocks > kMaxBlocks) blocks = kMaxBlocks;
-    hipLaunchKernelGGL((gemv_kernel<M, PRO, KC>), dim3(blocks), dim3(kThreads), 0, st, a);
+    const uint32_t cap = M * KC * 512u * 2u > 65536u ? kMaxBlocks / 2u : kMaxBlocks;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL((gemv_kernel<M, PRO, KC, SWI>), dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
-template <uint32_t PRO, uint32_t KC>
+template <uint32_t PRO, uint32_t KC, bool SWI = false>
 bool launch_gemv_m(uint32_t M, const GemvArgs& a, hipStream_t st) {
     switch (M) {
-        case 1: launch_gemv_t<1, PRO, KC>(a, st); return true;
-        case 2: launch_gemv_t<2, PRO, KC>(a, st); return true;
-        case 3: launch_gemv_t<3, PRO, KC>(a, st); return true;
-        case 4: launch_gemv_t<4, PRO, KC>(a, st); return true;
-        case 5: launch_gemv_t<5, PRO, KC>(a, st); return true;
-        case 6: launch_gemv_t<6, PRO, KC>(a, st); return true;
-        case 7: launch_gemv_t<7, PRO, KC>(a, st); return true;
-        case 8: launch_gemv_t<8, PRO, KC>(a, st); return true;
+        case 1: launch_gemv_t<1, PRO, KC, SWI>(a, st); return true;
+        case 2: launch_gemv_t<2, PRO, KC, SWI>(a, st); return true;
+        case 3: launch_gemv_t<3, PRO, KC, SWI>(a, st); return true;
+        case 4: launch_gemv_t<4, PRO, KC, SWI>(a, st); return true;
+        case 5: launch_gemv_t<5, PRO, KC, SWI>(a, st); return true;
+        case 6: launch_gemv_t<6, PRO, KC, SWI>(a, st); return true;
+        case 7: launch_gemv_t<7, PRO, KC, SWI>(a, st); return true;
+        case 8: launch_gemv_t<8, PRO, KC, SWI>(a, st); return true;
         default: return false;
     }
 }
@@ -446,6 +553,34 @@ extern "C" mc_status_t mc_model_gemv_resnorm(const uint16_t* d_w, const uint16_t
     return check_launch("gemv (residual + rmsnorm prologue) launch failed");
 }
 
+extern "C" mc_status_t mc_model_gemv_resnorm_swiglu(
+    const uint16_t* d_w, const uint16_t* d_res_in, const uint16_t* d_add,
+    const uint16_t* d_norm_w, uint16_t* d_res_out, uint32_t ldr, uint16_t* d_y, uint32_t ldy,
+    uint32_t M, uint32_t I, float eps, void* stream) {
+    TraceRange trace_range("mc_model_gemv_resnorm_swiglu");
+    if (d_w == nullptr || d_res_in == nullptr || d_norm_w == nullptr || d_y == nullptr ||
+        M == 0u || M > kMaxRows || I == 0u || ldr < 2048u || ldy < I || !(eps >= 0.f) ||
+        (d_res_out != nullptr && (d_res_out == d_res_in || d_res_out == d_add))) {
+        set_error("mc_model_gemv_resnorm_swiglu: invalid args (M=%u I=%u ldr=%u ldy=%u; the "
+                  "residual output must not alias its inputs)",
+                  M, I, ldr, ldy);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    GemvArgs a{};
+    a.w = d_w;
+    a.N = I;
+    a.res_in = d_res_in;
+    a.addend = d_add;
+    a.norm_w = d_norm_w;
+    a.res_out = d_res_out;
+    a.ldr = ldr;
+    a.eps = eps;
+    a.y = d_y;
+    a.ldy = ldy;
+    launch_gemv_m<kProResnorm, 4, true>(M, a, (hipStream_t)stream);
+    return check_launch("gemv (residual + rmsnorm prologue, swiglu epilogue) launch failed");
+}
+
 extern "C" mc_status_t mc_model_gemv_swiglu(const uint16_t* d_w, const uint16_t* d_gate_up,
                                             uint32_t ldx, uint16_t* d_y, uint32_t ldy,
                                             uint32_t M, uint32_t N, uint32_t K, void* stream) {
@@ -470,16 +605,26 @@ extern "C" mc_status_t mc_model_gemv_swiglu(const uint16_t* d_w, const uint16_t*
 
 extern "C" mc_status_t mc_model_argmax_bf16(const uint16_t* d_logits, uint32_t n,
                                             uint32_t rows, int32_t* d_out,
-                                            int32_t* const* d_slot_tok, void* stream) {
+                                            int32_t* const* d_slot_tok, float* d_stage_v,
+                                            int32_t* d_stage_i, void* stream) {
     TraceRange trace_range("mc_model_argmax_bf16");
-    if (d_logits == nullptr || n == 0u || rows == 0u ||
-        (d_out == nullptr) == (d_slot_tok == nullptr)) {
+    if (d_logits == nullptr || n == 0u || rows == 0u || rows > 65535u ||
+        (d_out == nullptr) == (d_slot_tok == nullptr) ||
+        (d_stage_v == nullptr) != (d_stage_i == nullptr)) {
         set_error("mc_model_argmax_bf16: invalid args (n=%u rows=%u, exactly one of out / "
-                  "slot_tok must be given)",
+                  "slot_tok must be given, stage buffers both or neither)",
                   n, rows);
         return MC_E_INVALID_ARGUMENT;
     }
-    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, (hipStream_t)stream, d_logits,
-                       n, d_out, d_slot_tok);
+    hipStream_t st = (hipStream_t)stream;
+    if (d_stage_v == nullptr) {
+        hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, st, d_logits, n, d_out,
+                           d_slot_tok);
+    } else {
+        hipLaunchKernelGGL(argmax_slices_kernel, dim3(kArgSlices, rows), dim3(256), 0, st,
+                           d_logits, n, d_stage_v, d_stage_i);
+        hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, st, d_stage_v, d_stage_i,
+                           d_out, d_slot_tok);
+    }
     return check_launch("argmax launch failed");
 }

@@ -118,6 +118,32 @@ def test_gemv_swiglu(lib, orc, dev, M, K):
     assert ok, st
 
 
+@pytest.mark.parametrize("M,I", [(1, 6144), (3, 6144), (8, 500)])
+def test_gemv_resnorm_swiglu(lib, orc, dev, M, I):
+    """gate_up projection with the norm prologue and the SwiGLU epilogue ==
+    the same projection rounded to bf16, then the SwiGLU."""
+    import torch
+    from oracle import model_ref as R
+    rng = np.random.default_rng(M * 7 + I)
+    w = rnd_bf16(orc, rng, (2 * I, 2048), 2048 ** -0.5)
+    res = rnd_bf16(orc, rng, (M, 2048), 2.0)
+    dlt = rnd_bf16(orc, rng, (M, 2048), 0.5)
+    g = orc.f32_to_bf16(1 + 0.1 * rng.standard_normal(2048, dtype=np.float32))
+    rout = torch.zeros(M * 2048, dtype=torch.int16, device=dev)
+    y = torch.zeros(M * I, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemv_resnorm_swiglu(P(to_dev(w, dev)), P(to_dev(res, dev)),
+                                            P(to_dev(dlt, dev)), P(to_dev(g, dev)), P(rout), 2048,
+                                            P(y), I, M, I, C.c_float(1e-6), stream()) == 0
+    torch.cuda.synchronize()
+    r = R.bf16(orc.bf16_to_f32(res) + orc.bf16_to_f32(dlt))
+    assert np.array_equal(from_dev(rout).reshape(M, 2048), orc.f32_to_bf16(r))
+    x = R.rmsnorm(r, orc.bf16_to_f32(g))
+    gu = R.bf16(x.astype(np.float64) @ orc.bf16_to_f32(w).astype(np.float64).T)
+    ref = R.silu_mul(gu[:, :I], gu[:, I:]).astype(np.float64)
+    ok, st = within_ulp(orc, from_dev(y).reshape(M, I), ref, ulps=2.0, frac=0.98)
+    assert ok, st
+
+
 def test_norm_swiglu_embedding_rows(lib, orc, dev):
     import torch
     from oracle import model_ref as R
@@ -167,12 +193,25 @@ def test_argmax(lib, orc, dev):
     lg = rnd_bf16(orc, rng, (3, n))
     lg[1, 70000] = lg[1, 1234] = orc.f32_to_bf16(np.float32([100.0]))[0]  # tie: lowest index
     lg[2, n - 1] = orc.f32_to_bf16(np.float32([50.0]))[0]
-    out = torch.full((3,), -1, dtype=torch.int32, device=dev)
-    assert lib.mc_model_argmax_bf16(P(to_dev(lg, dev)), n, 3, P(out), None, stream()) == 0
+    dlg = to_dev(lg, dev)
+    sv = torch.zeros(3 * 64, dtype=torch.float32, device=dev)
+    si = torch.zeros(3 * 64, dtype=torch.int32, device=dev)
+    for staged in (False, True):
+        out = torch.full((3,), -1, dtype=torch.int32, device=dev)
+        assert lib.mc_model_argmax_bf16(P(dlg), n, 3, P(out), None, P(sv) if staged else None,
+                                        P(si) if staged else None, stream()) == 0
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert got[0] == int(np.argmax(orc.bf16_to_f32(lg[0])))
+        assert got[1] == 1234 and got[2] == n - 1
+    # ties across slices: the lowest index wins
+    lg2 = np.zeros((1, n), dtype=np.uint16)
+    lg2[0, [n - 5, 3000, 70000]] = orc.f32_to_bf16(np.float32([7.0]))[0]
+    out = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    assert lib.mc_model_argmax_bf16(P(to_dev(lg2, dev)), n, 1, P(out), None, P(sv), P(si),
+                                    stream()) == 0
     torch.cuda.synchronize()
-    got = out.cpu().numpy()
-    assert got[0] == int(np.argmax(orc.bf16_to_f32(lg[0])))
-    assert got[1] == 1234 and got[2] == n - 1
+    assert int(out.cpu()[0]) == 3000
 
 
 # ---------------- whole model through the mc_* ABI ----------------

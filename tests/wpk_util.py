@@ -100,10 +100,16 @@ def arena_bytes(sections) -> int:
     return c
 
 
+def f32_to_bf16(x) -> np.ndarray:
+    """Nearest-even fp32 -> bf16 bits (finite inputs)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)) \
+        .astype(np.uint16)
+
+
 def random_blobs(seed: int, layer_sets: int = 2, scale: float = 1.0):
     """bf16 weight blobs (uint16) of a random model: embedding rows ~N(0, 1),
     projections ~N(0, 1/fan_in) * scale, norms ~1 + N(0, 0.1)."""
-    from oracle import f32_to_bf16
     rng = np.random.default_rng(seed)
 
     def mat(rows, cols, s):
@@ -125,7 +131,8 @@ def random_blobs(seed: int, layer_sets: int = 2, scale: float = 1.0):
 
 def weights_f32(sections, blobs):
     """Section name -> fp32 array (shared blobs are shared arrays)."""
-    from oracle import bf16_to_f32
+    def bf16_to_f32(b):
+        return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
     cache = {}
     out = {}
     for name, dims, k in sections:
