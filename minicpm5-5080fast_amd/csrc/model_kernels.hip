@@ -40,11 +40,11 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kMaxRows = MC_MODEL_GEMV_MAX_ROWS;  // activation rows per GEMV
-// GEMV grid: at most 512 workgroups (2 per CU on 256 CUs; 256 when the
-// staged activations need more than 64 KB of LDS), so every workgroup stages
-// its activation rows (and runs the norm prologue) once and then streams
-// rows; more workgroups only repeat the staging (measured: 2048 workgroups
-// made the 8-row gate_up projection 4x slower).
+// GEMV grid for several activation rows: at most 512 workgroups (2 per CU on
+// 256 CUs; 256 when the staged activations need more than 64 KB of LDS), so
+// every workgroup stages its activation rows (and runs the norm prologue)
+// once and then streams rows; more workgroups only repeat the staging
+// (measured: 2048 workgroups made the 8-row gate_up projection 4x slower).
 constexpr uint32_t kMaxBlocks = 512;
 
 __device__ __forceinline__ uint4 ld_stream(const uint16_t* p) {
@@ -200,6 +200,29 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
+    // The row is streamed in groups of kG chunks per lane (K / (512 kG) groups
+    // per row); the next group's loads (of this row or the next one) are
+    // issued before the current group is multiplied, so each lane keeps 2 kG
+    // 16-byte loads in flight whatever K is. The first group is requested
+    // before the activation prologue: the weights do not depend on it, so the
+    // two memory latencies overlap instead of adding up.
+    constexpr uint32_t kG = 4u, NG = KC / kG;
+    constexpr uint32_t R = SWI ? 2u : 1u;  // weight rows per output column
+    static_assert(KC % kG == 0u, "whole chunk groups");
+    const uint32_t stride = gridDim.x * 4u;
+    uint32_t n = blockIdx.x * 4u + wave, g = 0u;
+    const bool active = n < a.N;  // wave-uniform
+    auto load = [&](uint4 (&dst)[R][kG], uint32_t col, uint32_t grp) {
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+            for (uint32_t c = 0; c < kG; ++c)
+                dst[r][c] = ld_stream(a.w + (size_t)(col + r * a.N) * K +
+                                      8u * (lane + 64u * (grp * kG + c)));
+    };
+    uint4 wc[R][kG];
+    if (active) load(wc, n, g);
+
     // Stage the activation rows (after the prologue) into LDS.
     if constexpr (PRO == kProResnorm) {
         // all M rows' sums of squares in one workgroup reduction
@@ -251,27 +274,7 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvArgs a) {
         }
     }
     __syncthreads();
-
-    // The row is streamed in groups of kG chunks per lane (K / (512 kG) groups
-    // per row); the next group's loads (of this row or the next one) are
-    // issued before the current group is multiplied, so each lane keeps 2 kG
-    // 16-byte loads in flight whatever K is.
-    constexpr uint32_t kG = 4u, NG = KC / kG;
-    constexpr uint32_t R = SWI ? 2u : 1u;  // weight rows per output column
-    static_assert(KC % kG == 0u, "whole chunk groups");
-    const uint32_t stride = gridDim.x * 4u;
-    uint32_t n = blockIdx.x * 4u + wave, g = 0u;
-    if (n >= a.N) return;  // wave-uniform; no barrier follows
-    auto load = [&](uint4 (&dst)[R][kG], uint32_t col, uint32_t grp) {
-#pragma unroll
-        for (uint32_t r = 0; r < R; ++r)
-#pragma unroll
-            for (uint32_t c = 0; c < kG; ++c)
-                dst[r][c] = ld_stream(a.w + (size_t)(col + r * a.N) * K +
-                                      8u * (lane + 64u * (grp * kG + c)));
-    };
-    uint4 wc[R][kG];
-    load(wc, n, g);
+    if (!active) return;  // wave-uniform; no barrier follows
     float acc[R][M];
 #pragma unroll
     for (uint32_t r = 0; r < R; ++r)
@@ -428,7 +431,10 @@ __global__ void __launch_bounds__(1024)
 template <uint32_t M, uint32_t PRO, uint32_t KC, bool SWI>
 void launch_gemv_t(const GemvArgs& a, hipStream_t st) {
     uint32_t blocks = (a.N + 3u) / 4u;
-    const uint32_t cap = M * KC * 512u * 2u > 65536u ? kMaxBlocks / 2u : kMaxBlocks;
+    // one activation row: the prologue is short, so up to 1024 workgroups
+    // (one output row per wave for the 2560-row qkv projection)
+    const uint32_t cap = M == 1u ? 2u * kMaxBlocks
+                                 : (M * KC * 512u * 2u > 65536u ? kMaxBlocks / 2u : kMaxBlocks);
     if (blocks > cap) blocks = cap;
     hipLaunchKernelGGL((gemv_kernel<M, PRO, KC, SWI>), dim3(blocks), dim3(kThreads), 0, st, a);
 }
