@@ -17,7 +17,7 @@
 //     index (kernels.h:610, :641).
 //
 // MI355X design of the GEMV (decode is HBM-bound: every weight byte is read
-// once per token): a 256-thread workgroup first stages its activation rows
+// once per token): a workgroup first stages its activation rows
 // (after the fused prologue) into LDS, then each wave streams whole weight
 // rows, one row at a time, with the next row's loads issued before the
 // current row is reduced. Lane l reads the 16-byte chunks l, l + 64, ... of
@@ -40,12 +40,15 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kMaxRows = MC_MODEL_GEMV_MAX_ROWS;  // activation rows per GEMV
-// GEMV grid for several activation rows: at most 512 workgroups (2 per CU on
-// 256 CUs; 256 when the staged activations need more than 64 KB of LDS), so
-// every workgroup stages its activation rows (and runs the norm prologue)
-// once and then streams rows; more workgroups only repeat the staging
-// (measured: 2048 workgroups made the 8-row gate_up projection 4x slower).
-constexpr uint32_t kMaxBlocks = 512;
+// GEMV grids. One activation row: workgroups of 4 waves, up to 1024 of them
+// (one output column per wave for the 2560-column qkv projection); the
+// prologue is short. Several rows: every workgroup stages all rows (and runs
+// the norm prologue for each) before streaming columns, so the staging is
+// paid once per workgroup: one 8-wave workgroup per CU (measured against
+// 4 waves x 512 and 16 waves x 256: 8.7 / 9.3 / 16.9 us for the 8-row qkv
+// projection; 16 waves spill).
+constexpr uint32_t kSoloWaves = 4, kSoloBlocks = 1024;
+constexpr uint32_t kMultiWaves = 8, kMultiBlocks = 256;
 
 __device__ __forceinline__ uint4 ld_stream(const uint16_t* p) {
     return __builtin_bit_cast(uint4,
@@ -56,8 +59,11 @@ __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
 }
 __device__ __forceinline__ float lo_f(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float hi_f(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
+// Two fp32 -> bf16 round-to-nearest-even conversions in one v_cvt_pk_bf16_f32
+// (a in the low half).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
 // Sum over the 64 lanes, every lane receiving the total: xor 1 and xor 2
@@ -186,15 +192,15 @@ struct GemvArgs {
     uint32_t ldy;
 };
 
-// K = 512 * KC (16-byte chunks per lane per row). kProResnorm needs K = 2048
-// (one chunk per thread and row).
+// K = 512 * KC (16-byte chunks per lane per row); WV waves per workgroup,
+// one output column per wave at a time. kProResnorm needs K = 2048.
 // SWI: SwiGLU epilogue. Output column n (n < a.N) takes the weight rows n
 // (gate) and a.N + n (up) of a [2 a.N][K] matrix: y = bf16(silu(g) * u) with
 // g, u the two dot products rounded to bf16 first (the projection's output
 // rounding), as a gate_up projection followed by the SwiGLU kernel.
-template <uint32_t M, uint32_t PRO, uint32_t KC, bool SWI = false>
-__global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvArgs a) {
-    constexpr uint32_t K = 512u * KC, NCH = K / 8u;
+template <uint32_t M, uint32_t PRO, uint32_t KC, bool SWI, uint32_t WV>
+__global__ void __launch_bounds__(64u * WV) gemv_kernel(const GemvArgs a) {
+    constexpr uint32_t K = 512u * KC, NCH = K / 8u, T = 64u * WV;
     static_assert(PRO != kProResnorm || K == 2048u, "the norm prologue covers 2048 dims");
     __shared__ uint4 sx[M * NCH];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -209,8 +215,8 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvArgs a) {
     constexpr uint32_t kG = 4u, NG = KC / kG;
     constexpr uint32_t R = SWI ? 2u : 1u;  // weight rows per output column
     static_assert(KC % kG == 0u, "whole chunk groups");
-    const uint32_t stride = gridDim.x * 4u;
-    uint32_t n = blockIdx.x * 4u + wave, g = 0u;
+    const uint32_t stride = gridDim.x * WV;
+    uint32_t n = blockIdx.x * WV + wave, g = 0u;
     const bool active = n < a.N;  // wave-uniform
     auto load = [&](uint4 (&dst)[R][kG], uint32_t col, uint32_t grp) {
 #pragma unroll
@@ -225,48 +231,56 @@ __global__ void __launch_bounds__(kThreads) gemv_kernel(const GemvArgs a) {
 
     // Stage the activation rows (after the prologue) into LDS.
     if constexpr (PRO == kProResnorm) {
-        // all M rows' sums of squares in one workgroup reduction
+        // Item i = 256 m + c is the 16-byte chunk c of row m; a row's 256
+        // items are four whole waves, so each wave sums one row's part and
+        // all M rows' sums of squares come out of one workgroup barrier.
+        constexpr uint32_t IT = (M * 256u + T - 1u) / T;
         __shared__ float s_part[M][4];
-        uint4 v[M];
-        float ss[M];
+        uint4 v[IT];
 #pragma unroll
-        for (uint32_t m = 0; m < M; ++m) {
-            v[m] = ld16(a.res_in + (size_t)m * a.ldr + 8u * tid);
+        for (uint32_t it = 0; it < IT; ++it) {
+            const uint32_t i = tid + it * T;
+            if (i >= M * 256u) break;  // wave-uniform
+            const uint32_t m = i >> 8, c = i & 255u;
+            v[it] = ld16(a.res_in + (size_t)m * a.ldr + 8u * c);
             if (a.addend != nullptr) {
-                const uint4 d = ld16(a.addend + (size_t)m * a.ldr + 8u * tid);
-                v[m].x = pack2(lo_f(v[m].x) + lo_f(d.x), hi_f(v[m].x) + hi_f(d.x));
-                v[m].y = pack2(lo_f(v[m].y) + lo_f(d.y), hi_f(v[m].y) + hi_f(d.y));
-                v[m].z = pack2(lo_f(v[m].z) + lo_f(d.z), hi_f(v[m].z) + hi_f(d.z));
-                v[m].w = pack2(lo_f(v[m].w) + lo_f(d.w), hi_f(v[m].w) + hi_f(d.w));
+                const uint4 d = ld16(a.addend + (size_t)m * a.ldr + 8u * c);
+                v[it].x = pack2(lo_f(v[it].x) + lo_f(d.x), hi_f(v[it].x) + hi_f(d.x));
+                v[it].y = pack2(lo_f(v[it].y) + lo_f(d.y), hi_f(v[it].y) + hi_f(d.y));
+                v[it].z = pack2(lo_f(v[it].z) + lo_f(d.z), hi_f(v[it].z) + hi_f(d.z));
+                v[it].w = pack2(lo_f(v[it].w) + lo_f(d.w), hi_f(v[it].w) + hi_f(d.w));
             }
             if (a.res_out != nullptr && blockIdx.x == 0u)
-                *reinterpret_cast<uint4*>(a.res_out + (size_t)m * a.ldr + 8u * tid) = v[m];
-            const uint32_t u[4] = {v[m].x, v[m].y, v[m].z, v[m].w};
+                *reinterpret_cast<uint4*>(a.res_out + (size_t)m * a.ldr + 8u * c) = v[it];
+            const uint32_t u[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
             float t = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = lo_f(u[i]), q = hi_f(u[i]);
+            for (int j = 0; j < 4; ++j) {
+                const float p = lo_f(u[j]), q = hi_f(u[j]);
                 t = fmaf(p, p, t);
                 t = fmaf(q, q, t);
             }
-            ss[m] = wave_sum(t);
-            if (lane == 0u) s_part[m][wave] = ss[m];
+            t = wave_sum(t);
+            if (lane == 0u) s_part[m][c >> 6] = t;
         }
         __syncthreads();
-        const uint4 g = ld16(a.norm_w + 8u * tid);
 #pragma unroll
-        for (uint32_t m = 0; m < M; ++m) {
+        for (uint32_t it = 0; it < IT; ++it) {
+            const uint32_t i = tid + it * T;
+            if (i >= M * 256u) break;
+            const uint32_t m = i >> 8, c = i & 255u;
+            const uint4 g = ld16(a.norm_w + 8u * c);
             const float tot = ((s_part[m][0] + s_part[m][1]) + s_part[m][2]) + s_part[m][3];
             const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
             uint4 o;
-            o.x = pack2(lo_f(v[m].x) * inv * lo_f(g.x), hi_f(v[m].x) * inv * hi_f(g.x));
-            o.y = pack2(lo_f(v[m].y) * inv * lo_f(g.y), hi_f(v[m].y) * inv * hi_f(g.y));
-            o.z = pack2(lo_f(v[m].z) * inv * lo_f(g.z), hi_f(v[m].z) * inv * hi_f(g.z));
-            o.w = pack2(lo_f(v[m].w) * inv * lo_f(g.w), hi_f(v[m].w) * inv * hi_f(g.w));
-            sx[m * NCH + tid] = o;
+            o.x = pack2(lo_f(v[it].x) * inv * lo_f(g.x), hi_f(v[it].x) * inv * hi_f(g.x));
+            o.y = pack2(lo_f(v[it].y) * inv * lo_f(g.y), hi_f(v[it].y) * inv * hi_f(g.y));
+            o.z = pack2(lo_f(v[it].z) * inv * lo_f(g.z), hi_f(v[it].z) * inv * hi_f(g.z));
+            o.w = pack2(lo_f(v[it].w) * inv * lo_f(g.w), hi_f(v[it].w) * inv * hi_f(g.w));
+            sx[m * NCH + c] = o;
         }
     } else {
-        for (uint32_t i = tid; i < M * NCH; i += kThreads) {
+        for (uint32_t i = tid; i < M * NCH; i += T) {
             const uint32_t m = i / NCH, c = i % NCH;
             const uint16_t* xr = a.x + (size_t)m * a.ldx + 8u * c;
             if constexpr (PRO == kProSwiglu) sx[i] = swiglu8(ld16(xr), ld16(xr + K));
@@ -430,13 +444,12 @@ __global__ void __launch_bounds__(1024)
 
 template <uint32_t M, uint32_t PRO, uint32_t KC, bool SWI>
 void launch_gemv_t(const GemvArgs& a, hipStream_t st) {
-    uint32_t blocks = (a.N + 3u) / 4u;
-    // one activation row: the prologue is short, so up to 1024 workgroups
-    // (one output row per wave for the 2560-row qkv projection)
-    const uint32_t cap = M == 1u ? 2u * kMaxBlocks
-                                 : (M * KC * 512u * 2u > 65536u ? kMaxBlocks / 2u : kMaxBlocks);
+    constexpr uint32_t WV = M == 1u ? kSoloWaves : kMultiWaves;
+    constexpr uint32_t cap = M == 1u ? kSoloBlocks : kMultiBlocks;
+    uint32_t blocks = (a.N + WV - 1u) / WV;
     if (blocks > cap) blocks = cap;
-    hipLaunchKernelGGL((gemv_kernel<M, PRO, KC, SWI>), dim3(blocks), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((gemv_kernel<M, PRO, KC, SWI, WV>), dim3(blocks), dim3(64u * WV), 0, st,
+                       a);
 }
 
 template <uint32_t PRO, uint32_t KC, bool SWI = false>

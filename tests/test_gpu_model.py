@@ -144,6 +144,61 @@ def test_gemv_resnorm_swiglu(lib, orc, dev, M, I):
     assert ok, st
 
 
+def test_residual_rounding_specials(lib, orc, dev):
+    """The residual add rounds bf16 + bf16 in fp32 to bf16 with the oracle's
+    rule, bit for bit, on the cases a rounding shortcut would get wrong: exact
+    ties (both directions), carries into the exponent, overflow to infinity,
+    subnormals, signed zeros and infinities; a NaN operand gives a NaN of its
+    sign (the payload an fp32 add propagates is the platform's choice). Rows
+    go through the RMSNorm kernel and the fused GEMV prologue for one and for
+    several activation rows."""
+    import torch
+    f = np.float32
+    one_ulp = f(2.0 ** -7)
+    pairs = [(1.0, 2.0 ** -8), (1.0 + 2.0 ** -7, 2.0 ** -8), (-1.0, -(2.0 ** -8)),
+             (1.9921875, 2.0 ** -8), (3.3e38, 3.3e38), (-3.3e38, -3.3e38),
+             (1e-39, 1e-39), (-1e-40, 1e-40), (0.0, -0.0), (-0.0, -0.0),
+             (np.inf, 1.0), (-np.inf, 1.0), (1.0, one_ulp)]
+    res_f = np.array([p[0] for p in pairs], dtype=f)
+    add_f = np.array([p[1] for p in pairs], dtype=f)
+    res_b, add_b = orc.f32_to_bf16(res_f), orc.f32_to_bf16(add_f)
+    nan_bits = np.array([0x7FA5, 0xFF81, 0x7FC3], dtype=np.uint16)  # signalling, negative, quiet
+    res_b = np.concatenate([res_b, nan_bits, np.full(3, 0x3F80, np.uint16)])
+    add_b = np.concatenate([add_b, np.full(3, 0x3F80, np.uint16), nan_bits])
+    n = len(res_b)
+    rng = np.random.default_rng(5)
+    row_r = rnd_bf16(orc, rng, (2048,), 2.0)
+    row_a = rnd_bf16(orc, rng, (2048,), 0.5)
+    row_r[:n], row_a[:n] = res_b, add_b
+    want = orc.f32_to_bf16(orc.bf16_to_f32(row_r) + orc.bf16_to_f32(row_a))
+    g = orc.f32_to_bf16(np.ones(2048, dtype=f))
+    for M in (1, 3, 8):
+        res = np.tile(row_r, (M, 1))
+        dlt = np.tile(row_a, (M, 1))
+        # the norm kernel (in place)
+        dres, out = to_dev(res, dev), torch.zeros(M * 2048, dtype=torch.int16, device=dev)
+        assert lib.mc_model_rmsnorm_rows(P(dres), P(to_dev(dlt, dev)), P(to_dev(g, dev)), P(out),
+                                         M, 2048, C.c_float(1e-6), stream()) == 0
+        # the GEMV prologue
+        rout = torch.zeros(M * 2048, dtype=torch.int16, device=dev)
+        w = torch.zeros(64 * 2048, dtype=torch.int16, device=dev)
+        y = torch.zeros(M * 64, dtype=torch.int16, device=dev)
+        assert lib.mc_model_gemv_resnorm(P(w), P(to_dev(res, dev)), P(to_dev(dlt, dev)),
+                                         P(to_dev(g, dev)), P(rout), 2048, P(y), 64, M, 64,
+                                         C.c_float(1e-6), stream()) == 0
+        torch.cuda.synchronize()
+        nan = np.zeros(2048, dtype=bool)
+        nan[n - 6:n] = True
+        for got in (from_dev(dres), from_dev(rout)):
+            got = got.reshape(M, 2048).view(np.uint16)
+            for m in range(M):
+                assert np.array_equal(got[m][~nan], want[~nan]), \
+                    (M, m, [(hex(a), hex(b)) for a, b in zip(got[m][:n], want[:n])])
+                gn, wn = got[m][nan], want[nan]
+                assert np.all((gn & 0x7F80) == 0x7F80) and np.all(gn & 0x7F), [hex(v) for v in gn]
+                assert np.array_equal(gn & 0x8000, wn & 0x8000), [hex(v) for v in gn]
+
+
 def test_norm_swiglu_embedding_rows(lib, orc, dev):
     import torch
     from oracle import model_ref as R
