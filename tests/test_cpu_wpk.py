@@ -206,3 +206,37 @@ def test_forward_single_token_attention_is_v(orc):
     res = M.bf16(res + M.project(M.silu_mul(gu[:, :6144], gu[:, 6144:]), w["layer0.down"]))
     logits = M.project(M.rmsnorm(res, w["final_norm"]), w["lm_head"])[0]
     assert np.array_equal(ref.last_logits, logits)
+
+
+def test_forward_matches_reference_statement(orc):
+    """The oracle against the reference's own whole-model numpy statement
+    (tools/reference_forward.py MiniCPM5Ref; logits in
+    tests/golden/model_forward_small.json, written by
+    tests/golden/make_model_forward_golden.py): 2 layers, vocabulary 512,
+    random weights, a 6-token prefill and 5 greedy decode steps. The two
+    statements differ only where the reference leaves the arithmetic to
+    numpy (cos/sin of the RoPE angles, the fp32 softmax's summation order),
+    so most steps are bit-identical and every step's logits are within
+    relative L2 1e-2 with the same greedy token. A graph mistake (a norm
+    weight swapped, the residual added twice, the gate and up halves
+    exchanged, the wrong KV head for a query head) moves the logits by
+    order one."""
+    import json
+    from oracle import model_ref as M
+    with open(os.path.join(os.path.dirname(__file__), "golden",
+                           "model_forward_small.json")) as f:
+        d = json.load(f)
+    w = W.golden_small_model(d["seed"], d["vocab"], d["layers"])
+    ref = M.ModelRef({k: orc.bf16_to_f32(v) for k, v in w.items()}, d["layers"])
+    got = [(ref.forward(d["prompt"]), ref.last_logits)]
+    for _ in range(len(d["tokens"]) - 1):
+        ref.decode()
+        got.append((ref.next_token, ref.last_logits))
+    exact = 0
+    for step, (tok, logits) in enumerate(got):
+        want = orc.bf16_to_f32(np.array(d["logits_bf16"][step], dtype=np.uint16))
+        assert tok == d["tokens"][step], step
+        rel = np.linalg.norm(logits - want) / np.linalg.norm(want)
+        assert rel < 1e-2, (step, rel)
+        exact += int(np.array_equal(logits, want))
+    assert exact >= len(got) // 2, exact

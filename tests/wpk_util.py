@@ -140,3 +140,29 @@ def weights_f32(sections, blobs):
             cache[k] = bf16_to_f32(blobs[k]).reshape(dims)
         out[name] = cache[k]
     return out
+
+
+def golden_small_model(seed: int, vocab: int, layers: int):
+    """bf16 weights (uint16) of a small-vocabulary model of the full layer
+    shapes, generated from `seed` in a fixed order (the model-forward golden
+    fixture is made from these): embedding ~N(0, 1), projections
+    ~N(0, 1/fan_in), norms ~1 + N(0, 0.1)."""
+    rng = np.random.default_rng(seed)
+
+    def mat(rows, cols):
+        return f32_to_bf16(rng.standard_normal((rows, cols), dtype=np.float32)
+                           * np.float32(cols ** -0.5))
+
+    def norm():
+        return f32_to_bf16(1.0 + 0.1 * rng.standard_normal(HIDDEN, dtype=np.float32))
+
+    w = {"embedding": f32_to_bf16(rng.standard_normal((vocab, HIDDEN), dtype=np.float32)),
+         "lm_head": mat(vocab, HIDDEN), "final_norm": norm()}
+    for i in range(layers):
+        p = f"layer{i}."
+        w[p + "norm1"], w[p + "norm2"] = norm(), norm()
+        w[p + "qkv"] = mat(QKV, HIDDEN)
+        w[p + "o"] = mat(HIDDEN, HIDDEN)
+        w[p + "gate_up"] = mat(2 * INTER, HIDDEN)
+        w[p + "down"] = mat(HIDDEN, INTER)
+    return w
