@@ -20,7 +20,7 @@
 //     fused into the GEMV that consumes it (qkv, gate_up, lm_head) and the
 //     SwiGLU fused into the gate_up projection's output (each output column
 //     streams its gate and up rows together; the reference fuses it into the
-//     down projection's input, forward.cpp:165-190, which would repeat the
+//     down projection's input, forward.cpp:348-375, which would repeat the
 //     SwiGLU in every workgroup); the residual alternates between two
 //     buffers so that the workgroup writing the new residual never races the
 //     workgroups still reading the old one. Attention is the phase0 decode

@@ -267,6 +267,18 @@ def test_argmax(lib, orc, dev):
                                     stream()) == 0
     torch.cuda.synchronize()
     assert int(out.cpu()[0]) == 3000
+    # NaN never wins a comparison; an all-NaN row reports index 0
+    lg3 = rnd_bf16(orc, rng, (2, n))
+    lg3[0, ::7] = 0x7FC0
+    lg3[0, 99999] = orc.f32_to_bf16(np.float32([60.0]))[0]
+    lg3[1, :] = 0xFFC1
+    out = torch.full((2,), -1, dtype=torch.int32, device=dev)
+    for staged in (False, True):
+        assert lib.mc_model_argmax_bf16(P(to_dev(lg3, dev)), n, 2, P(out), None,
+                                        P(sv) if staged else None, P(si) if staged else None,
+                                        stream()) == 0
+        torch.cuda.synchronize()
+        assert out.cpu().tolist() == [99999, 0], staged
 
 
 # ---------------- whole model through the mc_* ABI ----------------
