@@ -212,7 +212,9 @@ __global__ void __launch_bounds__(64u * WV) gemv_kernel(const GemvArgs a) {
     // 16-byte loads in flight whatever K is. The first group is requested
     // before the activation prologue: the weights do not depend on it, so the
     // two memory latencies overlap instead of adding up.
-    constexpr uint32_t kG = 4u, NG = KC / kG;
+    // one activation row: the whole weight row is requested at once (12
+    // loads per lane for K = 6144); several rows: groups of 4 chunks
+    constexpr uint32_t kG = M == 1u ? KC : 4u, NG = KC / kG;
     constexpr uint32_t R = SWI ? 2u : 1u;  // weight rows per output column
     static_assert(KC % kG == 0u, "whole chunk groups");
     const uint32_t stride = gridDim.x * WV;
