@@ -535,6 +535,7 @@ def bench_model(pkg, torch, steps):
     import importlib
     import shutil
     import tempfile
+    import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     W = importlib.import_module("wpk_util")
     rt = importlib.import_module("minicpm5-5080fast_amd.runtime")
@@ -579,6 +580,38 @@ def bench_model(pkg, torch, steps):
         for x in ss + [s]:
             x.close()
         m.close()
+        # FP8 mode (precision MC_FP8): model_fp8.wpk beside model.wpk, e4m3
+        # codes of normal samples (fp32 bits cut to e4m3) with row scales;
+        # each decode streams the e4m3 projections and lm_head, 2.25 GB
+        rng = np.random.default_rng(8)
+        q8 = {}
+        for key, n, k in [(f"{nm}.{i}", nn, kk) for i in range(2) for nm, nn, kk in
+                          (("qkv", W.QKV, W.HIDDEN), ("o", W.HIDDEN, W.HIDDEN),
+                           ("gate_up", 2 * W.INTER, W.HIDDEN), ("down", W.HIDDEN, W.INTER))] + \
+                [("table", W.VOCAB, W.HIDDEN)]:
+            u = (rng.standard_normal((n, k), dtype=np.float32) * np.float32(64.0)).view(np.uint32)
+            e = ((u >> 23) & 0xFF).astype(np.int32) - 120
+            mag = np.where(e < 1, 0, np.minimum((e << 3) | ((u >> 20) & 7), 0x7E))
+            q8[key] = ((mag | ((u >> 24) & 0x80)).astype(np.uint8),
+                       np.full(n, 1.0 / (64.0 * k ** 0.5), dtype=np.float32))
+            del u, e, mag
+        secs8 = W.fp8_sections(2, lm_head=True)
+        W.write_fp8_wpk(os.path.join(d, "model_fp8.wpk"), secs8, q8)
+        del q8
+        fp8_bytes = W.fp8_arena_bytes(secs8)  # codes and scales, all read per decode
+        m = rt.Model(d, rt.model_options(max_context_tokens=8192, max_sessions=2,
+                                         enable_cuda_graph=1, precision=2))
+        s = rt.Session(m)
+        s.prefill(prompt)
+        for _ in range(3):
+            s.decode_one(cfg)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            s.decode_one(cfg)
+        solo8 = (time.perf_counter() - t0) / steps
+        s.close()
+        m.close()
     finally:
         shutil.rmtree(d, ignore_errors=True)
     return {
@@ -589,6 +622,9 @@ def bench_model(pkg, torch, steps):
         "decode_weight_gbs": weight_bytes / solo / 1e9,
         "decode_pct_hbm_peak": 100.0 * weight_bytes / solo / 1e9 / HBM_PEAK_GBS,
         "batch8_ms_per_step": batch * 1e3, "batch8_tokens_per_s": 8.0 / batch,
+        "fp8_decode_ms_per_token": solo8 * 1e3, "fp8_decode_tokens_per_s": 1.0 / solo8,
+        "fp8_weight_bytes_per_step": fp8_bytes,
+        "fp8_decode_weight_gbs": fp8_bytes / solo8 / 1e9,
     }
 
 

@@ -90,6 +90,43 @@ mc_status_t mc_model_gemv_swiglu(const uint16_t* d_w, const uint16_t* d_gate_up,
                                  uint16_t* d_y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
                                  void* stream);
 
+/* ---- FP8 projections (precision MC_FP8: single-token forwards) ----
+ * d_w: e4m3 codes [N][K] (uint8, 16-byte aligned rows), d_scale: fp32 [N]
+ * row scales; d_y[n] = bf16(d_scale[n] * sum_k e4m3(d_w[n][k]) * x[k])
+ * with fp32 accumulation, the scale applied after the sum (gemv_fp8.cu:3-7);
+ * e4m3 is s.eeee.mmm with bias 7, subnormals m/8 * 2^-6, and S.1111.111
+ * read as +-480 (kernels.h:120-148). One activation row (bf16); K is 2048
+ * or 6144. */
+
+/* launch_gemv_fp8 (kernels.h:721-726): x = d_x [K]. */
+mc_status_t mc_model_gemv_fp8(const uint8_t* d_w, const float* d_scale, const uint16_t* d_x,
+                              uint16_t* d_y, uint32_t N, uint32_t K, void* stream);
+
+/* launch_gemv_fp8_swiglu (kernels.h:753-758): x = SwiGLU of the gate|up row
+ * d_gate_up [2K], rounded to bf16. */
+mc_status_t mc_model_gemv_fp8_swiglu(const uint8_t* d_w, const float* d_scale,
+                                     const uint16_t* d_gate_up, uint16_t* d_y, uint32_t N,
+                                     uint32_t K, void* stream);
+
+/* launch_gemv_fp8_prologue (kernels.h:735-741): r = bf16(d_res_in + d_add)
+ * (d_add may be NULL), stored to d_res_out when not NULL (not aliasing the
+ * inputs), x = bf16(r * inv * d_norm_w) over 2048 dims, K = 2048. */
+mc_status_t mc_model_gemv_fp8_resnorm(const uint8_t* d_w, const float* d_scale,
+                                      const uint16_t* d_res_in, const uint16_t* d_add,
+                                      const uint16_t* d_norm_w, uint16_t* d_res_out,
+                                      uint16_t* d_y, uint32_t N, float eps, void* stream);
+
+/* The norm prologue with the SwiGLU epilogue of mc_model_gemv_resnorm_swiglu:
+ * d_w holds 2I rows (gate rows, then up rows) and d_scale 2I scales;
+ * d_y[n] = bf16(silu(g) * u) with g, u the two projections rounded to bf16
+ * (a gate_up projection, then the SwiGLU kernel). No reference counterpart
+ * (the reference fuses the SwiGLU into the down projection instead). */
+mc_status_t mc_model_gemv_fp8_resnorm_swiglu(const uint8_t* d_w, const float* d_scale,
+                                             const uint16_t* d_res_in, const uint16_t* d_add,
+                                             const uint16_t* d_norm_w, uint16_t* d_res_out,
+                                             uint16_t* d_y, uint32_t I, float eps,
+                                             void* stream);
+
 /* launch_sampling_greedy_bf16 (kernels.h:610) for rows == 1 and
  * launch_batch_argmax_bf16 (kernels.h:641): per row of n bf16 logits the
  * index of the largest value compared in fp32, ties to the lowest index,
@@ -110,6 +147,16 @@ mc_status_t mc_model_argmax_bf16(const uint16_t* d_logits, uint32_t n, uint32_t 
  * would hold in *arena_bytes, or MC_E_IO / MC_E_MODEL_MISMATCH with the
  * reason in mc_last_error(). No reference counterpart as a separate call. */
 mc_status_t mc_model_wpk_check(const char* path, uint64_t* arena_bytes);
+
+/* WeightLoader::load_wpk_fp8's checks (weight_loader.cpp:470-620) of a
+ * model_fp8.wpk without a device: the header rules of model.wpk, unique
+ * name hashes, the 42 x {qkv, o, gate_up, down} sections (plus "lm_head"
+ * when the package holds a dtype-2 one and MC_FP8_LMHEAD_OFF is unset) as
+ * dtype 2 (e4m3) row-major [N][K] with N * K code bytes and 4N scale bytes
+ * inside the file; other sections are ignored. *arena_bytes = the device
+ * bytes the codes and scales take. MC_E_MODEL_MISMATCH for a missing file
+ * or a failed check, MC_E_IO for a short read. */
+mc_status_t mc_model_wpk_fp8_check(const char* path, uint64_t* arena_bytes);
 
 /* Debug hooks of a model loaded with weights (outside the frozen ABI):
  * the bf16 logits (as fp32) of the last forward of a session (its last

@@ -92,6 +92,12 @@ _SIGS = {
                                                C.c_float, _P]),
     "mc_model_argmax_bf16": (C.c_int, [_P, _u32, _u32, _P, _P, _P, _P, _P]),
     "mc_model_wpk_check": (C.c_int, [C.c_char_p, C.POINTER(C.c_uint64)]),
+    "mc_model_wpk_fp8_check": (C.c_int, [C.c_char_p, C.POINTER(C.c_uint64)]),
+    "mc_model_gemv_fp8": (C.c_int, [_P, _P, _P, _P, _u32, _u32, _P]),
+    "mc_model_gemv_fp8_swiglu": (C.c_int, [_P, _P, _P, _P, _u32, _u32, _P]),
+    "mc_model_gemv_fp8_resnorm": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _u32, C.c_float, _P]),
+    "mc_model_gemv_fp8_resnorm_swiglu": (C.c_int, [_P, _P, _P, _P, _P, _P, _P, _u32,
+                                                   C.c_float, _P]),
 }
 
 

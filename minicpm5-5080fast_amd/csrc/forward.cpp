@@ -154,30 +154,57 @@ mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_ne
     uint16_t* cur = f.res_a;
     uint16_t* other = f.res_b;
     const uint16_t* pending = nullptr;
+    // FP8 mode (the FP8 package loaded): the four projections and, when the
+    // package has one, the lm_head on e4m3 weights (forward.cpp:117-130,
+    // 444-456)
+    const bool q8 = w.fp8_arena != nullptr;
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_tok, nullptr, cur, kHidden, 1, st));
     for (uint32_t l = 0; l < kModelLayers; ++l) {
         // qkv = W_qkv . norm1(cur + pending); the sum becomes the residual
-        FWD_OR_RETURN(mc_model_gemv_resnorm(w.qkv[l], cur, pending, w.norm1[l],
-                                            pending != nullptr ? other : nullptr, kHidden, f.qkv,
-                                            kQkvCols, 1, kQkvCols, kRmsEps, st));
+        uint16_t* res_out = pending != nullptr ? other : nullptr;
+        if (q8)
+            FWD_OR_RETURN(mc_model_gemv_fp8_resnorm(w.q_qkv[l], w.s_qkv[l], cur, pending,
+                                                    w.norm1[l], res_out, f.qkv, kQkvCols,
+                                                    kRmsEps, st));
+        else
+            FWD_OR_RETURN(mc_model_gemv_resnorm(w.qkv[l], cur, pending, w.norm1[l], res_out,
+                                                kHidden, f.qkv, kQkvCols, 1, kQkvCols, kRmsEps,
+                                                st));
         if (pending != nullptr) std::swap(cur, other);
         mark();
         FWD_OR_RETURN(mc_kv_attention_decode(f.qkv, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
                                              f.partials, f.max_chunks, f.attn, st, f.inv_freq,
                                              f.chunk_pos, f.partials2));
-        FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn, kHidden, f.o_out, kHidden, 1, kHidden, kHidden,
-                                    st));
-        FWD_OR_RETURN(mc_model_gemv_resnorm_swiglu(w.gate_up[l], cur, f.o_out, w.norm2[l], other,
-                                                   kHidden, f.mlp, kInter, 1, kInter, kRmsEps,
-                                                   st));
-        std::swap(cur, other);
-        FWD_OR_RETURN(mc_model_gemv(w.down[l], f.mlp, kInter, f.down, kHidden, 1, kHidden, kInter,
-                                    st));
+        if (q8) {
+            FWD_OR_RETURN(mc_model_gemv_fp8(w.q_o[l], w.s_o[l], f.attn, f.o_out, kHidden, kHidden,
+                                            st));
+            FWD_OR_RETURN(mc_model_gemv_fp8_resnorm_swiglu(w.q_gate_up[l], w.s_gate_up[l], cur,
+                                                           f.o_out, w.norm2[l], other, f.mlp,
+                                                           kInter, kRmsEps, st));
+            std::swap(cur, other);
+            FWD_OR_RETURN(mc_model_gemv_fp8(w.q_down[l], w.s_down[l], f.mlp, f.down, kHidden,
+                                            kInter, st));
+        } else {
+            FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn, kHidden, f.o_out, kHidden, 1, kHidden,
+                                        kHidden, st));
+            FWD_OR_RETURN(mc_model_gemv_resnorm_swiglu(w.gate_up[l], cur, f.o_out, w.norm2[l],
+                                                       other, kHidden, f.mlp, kInter, 1, kInter,
+                                                       kRmsEps, st));
+            std::swap(cur, other);
+            FWD_OR_RETURN(mc_model_gemv(w.down[l], f.mlp, kInter, f.down, kHidden, 1, kHidden,
+                                        kInter, st));
+        }
         pending = f.down;
         mark();
     }
-    FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur, pending, w.final_norm, nullptr, kHidden,
-                                        f.logits, kVocabSize, 1, kVocabSize, kRmsEps, st));
+    if (q8 && w.q_lm_head != nullptr)
+        FWD_OR_RETURN(mc_model_gemv_fp8_resnorm(w.q_lm_head, w.s_lm_head, cur, pending,
+                                                w.final_norm, nullptr, f.logits, kVocabSize,
+                                                kRmsEps, st));
+    else
+        FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur, pending, w.final_norm, nullptr,
+                                            kHidden, f.logits, kVocabSize, 1, kVocabSize,
+                                            kRmsEps, st));
     return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v, f.stage_i,
                                 st);
 }

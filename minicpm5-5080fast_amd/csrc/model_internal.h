@@ -31,12 +31,30 @@ struct ModelWeights {
     const uint16_t* norm2[kModelLayers] = {};
     const uint16_t* gate_up[kModelLayers] = {};  // [12288][2048], gate rows then up rows
     const uint16_t* down[kModelLayers] = {};     // [2048][6144]
+    // FP8 copies (model_fp8.wpk, precision MC_FP8): e4m3 codes [N][K] and
+    // fp32 row scales [N] of the four projections, and of the lm_head when
+    // the package holds one; fp8_arena == nullptr when not loaded.
+    void* fp8_arena = nullptr;
+    uint64_t fp8_bytes = 0;
+    const uint8_t* q_qkv[kModelLayers] = {};
+    const float* s_qkv[kModelLayers] = {};
+    const uint8_t* q_o[kModelLayers] = {};
+    const float* s_o[kModelLayers] = {};
+    const uint8_t* q_gate_up[kModelLayers] = {};
+    const float* s_gate_up[kModelLayers] = {};
+    const uint8_t* q_down[kModelLayers] = {};
+    const float* s_down[kModelLayers] = {};
+    const uint8_t* q_lm_head = nullptr;
+    const float* s_lm_head = nullptr;
 };
 
 // Reads and checks `path` (a model.wpk). With `w` != nullptr the sections
 // are uploaded into one device allocation on the current device (stream
 // `st`), otherwise only checked; *arena_bytes receives the allocation size.
 mc_status_t wpk_load(const char* path, ModelWeights* w, uint64_t* arena_bytes, hipStream_t st);
+// The same for model_fp8.wpk into w's FP8 members (its own allocation).
+mc_status_t wpk_load_fp8(const char* path, ModelWeights* w, uint64_t* arena_bytes,
+                         hipStream_t st);
 void wpk_free(ModelWeights* w);
 
 }  // namespace mckv

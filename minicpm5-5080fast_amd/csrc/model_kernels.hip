@@ -192,6 +192,79 @@ struct GemvArgs {
     uint32_t ldy;
 };
 
+// Stages M activation rows of K bf16 into LDS sx[M][K / 8] (16-byte chunks)
+// with block T threads: plain (x rows of stride ldx), SwiGLU of gate|up rows,
+// or residual add + RMSNorm (K = 2048: r = bf16(res_in + addend) stored to
+// res_out by workgroup 0 when not null, x = bf16(r * inv * norm_w); all M
+// rows' sums of squares in one workgroup reduction). The caller
+// synchronizes before reading sx.
+template <uint32_t M, uint32_t PRO, uint32_t K, uint32_t T>
+__device__ __forceinline__ void stage_rows(const uint16_t* x, uint32_t ldx,
+                                           const uint16_t* res_in, const uint16_t* addend,
+                                           const uint16_t* norm_w, uint16_t* res_out,
+                                           uint32_t ldr, float eps, uint4* sx) {
+    constexpr uint32_t NCH = K / 8u;
+    static_assert(PRO != kProResnorm || K == 2048u, "the norm prologue covers 2048 dims");
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    if constexpr (PRO == kProResnorm) {
+        // Item i = 256 m + c is the 16-byte chunk c of row m; a row's 256
+        // items are four whole waves, so each wave sums one row's part and
+        // all M rows' sums of squares come out of one workgroup barrier.
+        constexpr uint32_t IT = (M * 256u + T - 1u) / T;
+        __shared__ float s_part[M][4];
+        uint4 v[IT];
+#pragma unroll
+        for (uint32_t it = 0; it < IT; ++it) {
+            const uint32_t i = tid + it * T;
+            if (i >= M * 256u) break;  // wave-uniform
+            const uint32_t m = i >> 8, c = i & 255u;
+            v[it] = ld16(res_in + (size_t)m * ldr + 8u * c);
+            if (addend != nullptr) {
+                const uint4 d = ld16(addend + (size_t)m * ldr + 8u * c);
+                v[it].x = pack2(lo_f(v[it].x) + lo_f(d.x), hi_f(v[it].x) + hi_f(d.x));
+                v[it].y = pack2(lo_f(v[it].y) + lo_f(d.y), hi_f(v[it].y) + hi_f(d.y));
+                v[it].z = pack2(lo_f(v[it].z) + lo_f(d.z), hi_f(v[it].z) + hi_f(d.z));
+                v[it].w = pack2(lo_f(v[it].w) + lo_f(d.w), hi_f(v[it].w) + hi_f(d.w));
+            }
+            if (res_out != nullptr && blockIdx.x == 0u)
+                *reinterpret_cast<uint4*>(res_out + (size_t)m * ldr + 8u * c) = v[it];
+            const uint32_t u[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+            float t = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float p = lo_f(u[j]), q = hi_f(u[j]);
+                t = fmaf(p, p, t);
+                t = fmaf(q, q, t);
+            }
+            t = wave_sum(t);
+            if (lane == 0u) s_part[m][c >> 6] = t;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t it = 0; it < IT; ++it) {
+            const uint32_t i = tid + it * T;
+            if (i >= M * 256u) break;
+            const uint32_t m = i >> 8, c = i & 255u;
+            const uint4 g = ld16(norm_w + 8u * c);
+            const float tot = ((s_part[m][0] + s_part[m][1]) + s_part[m][2]) + s_part[m][3];
+            const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+            uint4 o;
+            o.x = pack2(lo_f(v[it].x) * inv * lo_f(g.x), hi_f(v[it].x) * inv * hi_f(g.x));
+            o.y = pack2(lo_f(v[it].y) * inv * lo_f(g.y), hi_f(v[it].y) * inv * hi_f(g.y));
+            o.z = pack2(lo_f(v[it].z) * inv * lo_f(g.z), hi_f(v[it].z) * inv * hi_f(g.z));
+            o.w = pack2(lo_f(v[it].w) * inv * lo_f(g.w), hi_f(v[it].w) * inv * hi_f(g.w));
+            sx[m * NCH + c] = o;
+        }
+    } else {
+        for (uint32_t i = tid; i < M * NCH; i += T) {
+            const uint32_t m = i / NCH, c = i % NCH;
+            const uint16_t* xr = x + (size_t)m * ldx + 8u * c;
+            if constexpr (PRO == kProSwiglu) sx[i] = swiglu8(ld16(xr), ld16(xr + K));
+            else sx[i] = ld16(xr);
+        }
+    }
+}
+
 // K = 512 * KC (16-byte chunks per lane per row); WV waves per workgroup,
 // one output column per wave at a time. kProResnorm needs K = 2048.
 // SWI: SwiGLU epilogue. Output column n (n < a.N) takes the weight rows n
@@ -231,64 +304,8 @@ __global__ void __launch_bounds__(64u * WV) gemv_kernel(const GemvArgs a) {
     uint4 wc[R][kG];
     if (active) load(wc, n, g);
 
-    // Stage the activation rows (after the prologue) into LDS.
-    if constexpr (PRO == kProResnorm) {
-        // Item i = 256 m + c is the 16-byte chunk c of row m; a row's 256
-        // items are four whole waves, so each wave sums one row's part and
-        // all M rows' sums of squares come out of one workgroup barrier.
-        constexpr uint32_t IT = (M * 256u + T - 1u) / T;
-        __shared__ float s_part[M][4];
-        uint4 v[IT];
-#pragma unroll
-        for (uint32_t it = 0; it < IT; ++it) {
-            const uint32_t i = tid + it * T;
-            if (i >= M * 256u) break;  // wave-uniform
-            const uint32_t m = i >> 8, c = i & 255u;
-            v[it] = ld16(a.res_in + (size_t)m * a.ldr + 8u * c);
-            if (a.addend != nullptr) {
-                const uint4 d = ld16(a.addend + (size_t)m * a.ldr + 8u * c);
-                v[it].x = pack2(lo_f(v[it].x) + lo_f(d.x), hi_f(v[it].x) + hi_f(d.x));
-                v[it].y = pack2(lo_f(v[it].y) + lo_f(d.y), hi_f(v[it].y) + hi_f(d.y));
-                v[it].z = pack2(lo_f(v[it].z) + lo_f(d.z), hi_f(v[it].z) + hi_f(d.z));
-                v[it].w = pack2(lo_f(v[it].w) + lo_f(d.w), hi_f(v[it].w) + hi_f(d.w));
-            }
-            if (a.res_out != nullptr && blockIdx.x == 0u)
-                *reinterpret_cast<uint4*>(a.res_out + (size_t)m * a.ldr + 8u * c) = v[it];
-            const uint32_t u[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-            float t = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float p = lo_f(u[j]), q = hi_f(u[j]);
-                t = fmaf(p, p, t);
-                t = fmaf(q, q, t);
-            }
-            t = wave_sum(t);
-            if (lane == 0u) s_part[m][c >> 6] = t;
-        }
-        __syncthreads();
-#pragma unroll
-        for (uint32_t it = 0; it < IT; ++it) {
-            const uint32_t i = tid + it * T;
-            if (i >= M * 256u) break;
-            const uint32_t m = i >> 8, c = i & 255u;
-            const uint4 g = ld16(a.norm_w + 8u * c);
-            const float tot = ((s_part[m][0] + s_part[m][1]) + s_part[m][2]) + s_part[m][3];
-            const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
-            uint4 o;
-            o.x = pack2(lo_f(v[it].x) * inv * lo_f(g.x), hi_f(v[it].x) * inv * hi_f(g.x));
-            o.y = pack2(lo_f(v[it].y) * inv * lo_f(g.y), hi_f(v[it].y) * inv * hi_f(g.y));
-            o.z = pack2(lo_f(v[it].z) * inv * lo_f(g.z), hi_f(v[it].z) * inv * hi_f(g.z));
-            o.w = pack2(lo_f(v[it].w) * inv * lo_f(g.w), hi_f(v[it].w) * inv * hi_f(g.w));
-            sx[m * NCH + c] = o;
-        }
-    } else {
-        for (uint32_t i = tid; i < M * NCH; i += T) {
-            const uint32_t m = i / NCH, c = i % NCH;
-            const uint16_t* xr = a.x + (size_t)m * a.ldx + 8u * c;
-            if constexpr (PRO == kProSwiglu) sx[i] = swiglu8(ld16(xr), ld16(xr + K));
-            else sx[i] = ld16(xr);
-        }
-    }
+    stage_rows<M, PRO, K, T>(a.x, a.ldx, a.res_in, a.addend, a.norm_w, a.res_out, a.ldr, a.eps,
+                             sx);
     __syncthreads();
     if (!active) return;  // wave-uniform; no barrier follows
     float acc[R][M];
@@ -353,6 +370,167 @@ __global__ void __launch_bounds__(64u * WV) gemv_kernel(const GemvArgs a) {
         n = n2;
         g = g2;
     }
+}
+
+// ---- FP8 GEMV (one activation row) ----
+// y[n] = bf16(scale[n] * sum_k e4m3(w[n][k]) x[k]) with fp32 accumulation,
+// the row scale applied after the sum. Weights: uint8 e4m3 [N][K] rows
+// (K / 16 16-byte chunks), lane l of a wave reading chunks l, l + 64, ...
+// of each row it takes (KC8 = K / 1024 per lane; 1 KB per wave load). The
+// activation row is staged once per workgroup through the prologue into LDS
+// (stage_rows, as the bf16 GEMV) when the norm prologue runs, and read by
+// each lane directly otherwise; a lane's chunks are the same for every row,
+// so it keeps its K / 64 activation values in registers (fp32) and every
+// row is one weight load round and 16 FMAs per chunk. e4m3 -> fp32 is v_cvt_pk_f32_fp8 (exact); the codes S.1111.111,
+// which it reads as NaN, are decoded by the bit layout instead (+-480) in a
+// rarely taken branch, so every code has the meaning of the oracle's decoder.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float e4m3_bits_to_f32(uint32_t b) {
+    // exponent field e, mantissa m: e = 0 -> m/8 * 2^-6, else (1 + m/8) 2^(e-7)
+    // (the fp32 with the 7 magnitude bits at bit 20 is that value * 2^-120)
+    const float mag = __uint_as_float((b & 0x7Fu) << 20) * 0x1p120f;
+    return (b & 0x80u) ? -mag : mag;
+}
+
+__device__ __forceinline__ void fp8x16_fma(const uint4& w, const float* x, float& s0,
+                                           float& s1) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+    uint32_t nan_code = 0u;  // a byte 0x7F or 0xFF in the chunk
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nan_code |= ((u[i] & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u;
+    if (nan_code == 0u) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)u[i], false);
+            const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)u[i], true);
+            s0 = fmaf(lo[0], x[4 * i + 0], s0);
+            s1 = fmaf(lo[1], x[4 * i + 1], s1);
+            s0 = fmaf(hi[0], x[4 * i + 2], s0);
+            s1 = fmaf(hi[1], x[4 * i + 3], s1);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s0 = fmaf(e4m3_bits_to_f32(u[i] & 0xFFu), x[4 * i + 0], s0);
+            s1 = fmaf(e4m3_bits_to_f32((u[i] >> 8) & 0xFFu), x[4 * i + 1], s1);
+            s0 = fmaf(e4m3_bits_to_f32((u[i] >> 16) & 0xFFu), x[4 * i + 2], s0);
+            s1 = fmaf(e4m3_bits_to_f32(u[i] >> 24), x[4 * i + 3], s1);
+        }
+    }
+}
+
+struct Gemv8Args {
+    const uint8_t* w;      // [N][K] (SwiGLU epilogue: [2N][K], gate rows then up rows)
+    const float* scale;    // [N] ([2N])
+    uint32_t N;
+    const uint16_t* x;     // kProNone: [K]; kProSwiglu: gate|up [2K]
+    const uint16_t* res_in;  // kProResnorm: [2048]
+    const uint16_t* addend;  // kProResnorm: [2048] or nullptr
+    const uint16_t* norm_w;  // kProResnorm: [2048]
+    uint16_t* res_out;       // kProResnorm: [2048] (workgroup 0) or nullptr
+    float eps;
+    uint16_t* y;  // [N]
+};
+
+// Waves (output rows in flight) per workgroup: 8 with the norm prologue,
+// whose staging is shared by the workgroup's waves; 4 otherwise (measured:
+// 8-row qkv-shape norm prologue 3.98 us with 8 waves against 4.24 with 4;
+// plain o 2.85 us with direct loads against 3.10 staged).
+template <uint32_t PRO>
+constexpr uint32_t f8_waves() { return PRO == kProResnorm ? 8u : 4u; }
+
+template <uint32_t PRO, uint32_t KC8, bool SWI>
+__global__ void __launch_bounds__(64u * f8_waves<PRO>()) gemv8_kernel(const Gemv8Args a) {
+    constexpr uint32_t kF8Waves = f8_waves<PRO>();
+    constexpr uint32_t K = 1024u * KC8;
+    constexpr uint32_t R = SWI ? 2u : 1u;
+    static_assert(PRO != kProResnorm || K == 2048u, "the norm prologue covers 2048 dims");
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t stride = gridDim.x * kF8Waves;
+    uint32_t n = blockIdx.x * kF8Waves + wave;
+    const bool active = n < a.N;  // wave-uniform
+    auto load = [&](uint4 (&dst)[R][KC8], uint32_t col) {
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+            for (uint32_t c = 0; c < KC8; ++c)
+                dst[r][c] = ld_stream(reinterpret_cast<const uint16_t*>(
+                    a.w + (size_t)(col + r * a.N) * K + 16u * (lane + 64u * c)));
+    };
+    // the first row's loads go out before the activation prologue
+    uint4 wc[R][KC8];
+    if (active) load(wc, n);
+    // this lane's activation values k = 16 (lane + 64 c) + j, as fp32: with
+    // the norm prologue from the row staged once per workgroup in LDS, else
+    // read directly (the SwiGLU applied per lane)
+    __shared__ uint4 sx[PRO == kProResnorm ? K / 8u : 1u];
+    if constexpr (PRO == kProResnorm) {
+        stage_rows<1u, PRO, K, 64u * kF8Waves>(nullptr, 0u, a.res_in, a.addend, a.norm_w,
+                                               a.res_out, 0u, a.eps, sx);
+        __syncthreads();
+    }
+    if (!active) return;  // wave-uniform; no barrier follows
+    float x[KC8][16];
+#pragma unroll
+    for (uint32_t c = 0; c < KC8; ++c)
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; ++h) {
+            uint4 t;
+            if constexpr (PRO == kProResnorm) {
+                t = sx[2u * (lane + 64u * c) + h];
+            } else {
+                const uint16_t* xp = a.x + 16u * (lane + 64u * c) + 8u * h;
+                if constexpr (PRO == kProSwiglu) t = swiglu8(ld16(xp), ld16(xp + K));
+                else t = ld16(xp);
+            }
+            const uint32_t u[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[c][8 * h + 2 * i] = lo_f(u[i]);
+                x[c][8 * h + 2 * i + 1] = hi_f(u[i]);
+            }
+        }
+
+    while (true) {
+        const uint32_t n2 = n + stride;
+        const bool more = n2 < a.N;
+        uint4 wn[R][KC8];
+        if (more) load(wn, n2);
+        float acc[R];
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (uint32_t c = 0; c < KC8; ++c) fp8x16_fma(wc[r][c], x[c], s0, s1);
+            acc[r] = wave_sum(s0 + s1);
+        }
+        float v = acc[0] * a.scale[n];
+        if constexpr (SWI) {
+            const float gt = bf16_to_f32(f32_to_bf16(v));
+            const float up = bf16_to_f32(f32_to_bf16(acc[1] * a.scale[a.N + n]));
+            v = silu_mul(gt, up);
+        }
+        if (lane == 0u) a.y[n] = f32_to_bf16(v);
+        if (!more) break;
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+            for (uint32_t c = 0; c < KC8; ++c) wc[r][c] = wn[r][c];
+        n = n2;
+    }
+}
+
+// One wave per output row, 4 per workgroup; at most 1024 workgroups (the
+// 130560-row lm_head: ~32 rows per wave, the next row's loads in flight).
+template <uint32_t PRO, uint32_t KC8, bool SWI>
+void launch_gemv8(const Gemv8Args& a, hipStream_t st) {
+    constexpr uint32_t kF8Waves = f8_waves<PRO>();
+    uint32_t blocks = (a.N + kF8Waves - 1u) / kF8Waves;
+    if (blocks > 4096u / kF8Waves) blocks = 4096u / kF8Waves;
+    hipLaunchKernelGGL((gemv8_kernel<PRO, KC8, SWI>), dim3(blocks), dim3(64u * kF8Waves), 0, st,
+                       a);
 }
 
 // ---- greedy argmax over bf16 logits ----
@@ -648,4 +826,101 @@ extern "C" mc_status_t mc_model_argmax_bf16(const uint16_t* d_logits, uint32_t n
                            d_out, d_slot_tok);
     }
     return check_launch("argmax launch failed");
+}
+
+extern "C" mc_status_t mc_model_gemv_fp8(const uint8_t* d_w, const float* d_scale,
+                                         const uint16_t* d_x, uint16_t* d_y, uint32_t N,
+                                         uint32_t K, void* stream) {
+    TraceRange trace_range("mc_model_gemv_fp8");
+    if (d_w == nullptr || d_scale == nullptr || d_x == nullptr || d_y == nullptr || N == 0u ||
+        (K != 2048u && K != 6144u) || ((uintptr_t)d_w & 15u) != 0u) {
+        set_error("mc_model_gemv_fp8: invalid args (N=%u K=%u; K 2048 or 6144, weights "
+                  "16-byte aligned)",
+                  N, K);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    Gemv8Args a{};
+    a.w = d_w;
+    a.scale = d_scale;
+    a.N = N;
+    a.x = d_x;
+    a.y = d_y;
+    if (K == 2048u) launch_gemv8<kProNone, 2, false>(a, (hipStream_t)stream);
+    else launch_gemv8<kProNone, 6, false>(a, (hipStream_t)stream);
+    return check_launch("fp8 gemv launch failed");
+}
+
+extern "C" mc_status_t mc_model_gemv_fp8_swiglu(const uint8_t* d_w, const float* d_scale,
+                                                const uint16_t* d_gate_up, uint16_t* d_y,
+                                                uint32_t N, uint32_t K, void* stream) {
+    TraceRange trace_range("mc_model_gemv_fp8_swiglu");
+    if (d_w == nullptr || d_scale == nullptr || d_gate_up == nullptr || d_y == nullptr ||
+        N == 0u || (K != 2048u && K != 6144u) || ((uintptr_t)d_w & 15u) != 0u) {
+        set_error("mc_model_gemv_fp8_swiglu: invalid args (N=%u K=%u)", N, K);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    Gemv8Args a{};
+    a.w = d_w;
+    a.scale = d_scale;
+    a.N = N;
+    a.x = d_gate_up;
+    a.y = d_y;
+    if (K == 2048u) launch_gemv8<kProSwiglu, 2, false>(a, (hipStream_t)stream);
+    else launch_gemv8<kProSwiglu, 6, false>(a, (hipStream_t)stream);
+    return check_launch("fp8 gemv (swiglu prologue) launch failed");
+}
+
+extern "C" mc_status_t mc_model_gemv_fp8_resnorm(const uint8_t* d_w, const float* d_scale,
+                                                 const uint16_t* d_res_in,
+                                                 const uint16_t* d_add,
+                                                 const uint16_t* d_norm_w,
+                                                 uint16_t* d_res_out, uint16_t* d_y,
+                                                 uint32_t N, float eps, void* stream) {
+    TraceRange trace_range("mc_model_gemv_fp8_resnorm");
+    if (d_w == nullptr || d_scale == nullptr || d_res_in == nullptr || d_norm_w == nullptr ||
+        d_y == nullptr || N == 0u || !(eps >= 0.f) || ((uintptr_t)d_w & 15u) != 0u ||
+        (d_res_out != nullptr && (d_res_out == d_res_in || d_res_out == d_add))) {
+        set_error("mc_model_gemv_fp8_resnorm: invalid args (N=%u eps=%g; res_out must not "
+                  "alias res_in or add)",
+                  N, (double)eps);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    Gemv8Args a{};
+    a.w = d_w;
+    a.scale = d_scale;
+    a.N = N;
+    a.res_in = d_res_in;
+    a.addend = d_add;
+    a.norm_w = d_norm_w;
+    a.res_out = d_res_out;
+    a.eps = eps;
+    a.y = d_y;
+    launch_gemv8<kProResnorm, 2, false>(a, (hipStream_t)stream);
+    return check_launch("fp8 gemv (norm prologue) launch failed");
+}
+
+extern "C" mc_status_t mc_model_gemv_fp8_resnorm_swiglu(
+    const uint8_t* d_w, const float* d_scale, const uint16_t* d_res_in, const uint16_t* d_add,
+    const uint16_t* d_norm_w, uint16_t* d_res_out, uint16_t* d_y, uint32_t I, float eps,
+    void* stream) {
+    TraceRange trace_range("mc_model_gemv_fp8_resnorm_swiglu");
+    if (d_w == nullptr || d_scale == nullptr || d_res_in == nullptr || d_norm_w == nullptr ||
+        d_y == nullptr || I == 0u || !(eps >= 0.f) || ((uintptr_t)d_w & 15u) != 0u ||
+        (d_res_out != nullptr && (d_res_out == d_res_in || d_res_out == d_add))) {
+        set_error("mc_model_gemv_fp8_resnorm_swiglu: invalid args (I=%u eps=%g)", I,
+                  (double)eps);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    Gemv8Args a{};
+    a.w = d_w;
+    a.scale = d_scale;
+    a.N = I;
+    a.res_in = d_res_in;
+    a.addend = d_add;
+    a.norm_w = d_norm_w;
+    a.res_out = d_res_out;
+    a.eps = eps;
+    a.y = d_y;
+    launch_gemv8<kProResnorm, 2, true>(a, (hipStream_t)stream);
+    return check_launch("fp8 gemv (norm prologue, swiglu epilogue) launch failed");
 }

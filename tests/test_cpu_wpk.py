@@ -125,6 +125,71 @@ def test_layer_window_switches_rejected(lib, tmp_path, monkeypatch):
     assert st == UNSUPPORTED and "MC_LOAD_LAYERS_MAX" in msg, msg
 
 
+# ---------------- model_fp8.wpk (precision MC_FP8) ----------------
+
+def check8(lib, path):
+    n = C.c_uint64(0)
+    st = lib.mc_model_wpk_fp8_check(str(path).encode(), C.byref(n))
+    return st, n.value, lib.mc_last_error().decode()
+
+
+def test_fp8_package_valid(lib, tmp_path, monkeypatch):
+    """The 168 projections plus the optional lm_head (weight_loader.cpp:
+    525-560); sections the FP8 loader does not use are ignored; with
+    MC_FP8_LMHEAD_OFF set a package's lm_head is skipped."""
+    p = tmp_path / "model_fp8.wpk"
+    secs = W.fp8_sections(lm_head=True)
+    W.write_fp8_wpk(p, secs, W.fp8_sparse_blobs())
+    st, n, msg = check8(lib, p)
+    assert st == OK, msg
+    assert n == W.fp8_arena_bytes(secs)
+    assert 2.2e9 < n < 2.3e9  # half the bytes of the bf16 projections and lm_head
+    monkeypatch.setenv("MC_FP8_LMHEAD_OFF", "1")
+    st, n_off, msg = check8(lib, p)
+    assert st == OK and n_off == W.fp8_arena_bytes(secs[:-1]), msg
+    monkeypatch.delenv("MC_FP8_LMHEAD_OFF")
+    secs = W.fp8_sections(lm_head=False)
+    W.write_fp8_wpk(p, secs + [("layer0.norm1", (1, 2048), "o.0")], W.fp8_sparse_blobs())
+    st, n, msg = check8(lib, p)
+    assert st == OK and n == W.fp8_arena_bytes(secs), msg
+
+
+@pytest.mark.parametrize("patch", [
+    lambda d: d.update(dtype=0), lambda d: d.update(layout=1), lambda d: d.update(rank=1),
+    lambda d: d["dims"].__setitem__(1, 2049), lambda d: d.update(bytes=d["bytes"] - 1),
+    lambda d: d.update(scale_bytes=d["scale_bytes"] + 4), lambda d: d.update(offset=64),
+    lambda d: d.update(scale_offset=1 << 42), lambda d: d.update(hash=W.fnv1a64("layer3.oo"))])
+def test_fp8_package_bad_entry(lib, tmp_path, patch):
+    p = tmp_path / "model_fp8.wpk"
+
+    def ep(i, d):
+        if i == 13:  # layer3.o
+            patch(d)
+    W.write_fp8_wpk(p, W.fp8_sections(), W.fp8_sparse_blobs(), entry_patch=ep)
+    st, _, msg = check8(lib, p)
+    assert st == MISMATCH and "layer3.o" in msg, msg
+
+
+def test_fp8_package_header_duplicates_and_missing_file(lib, tmp_path):
+    p = tmp_path / "model_fp8.wpk"
+    assert check8(lib, p)[0] == MISMATCH  # no package: MC_FP8 cannot load
+    secs = W.fp8_sections()
+
+    def dup(i, d):
+        if i == 5:
+            d["hash"] = W.fnv1a64("layer0.qkv")
+    W.write_fp8_wpk(p, secs, W.fp8_sparse_blobs(), entry_patch=dup)
+    st, _, msg = check8(lib, p)
+    assert st == MISMATCH and "share" in msg, msg
+    W.write_fp8_wpk(p, secs, W.fp8_sparse_blobs())
+    with open(p, "r+b") as f:
+        f.write(b"MKP0")
+    assert check8(lib, p)[0] == MISMATCH
+    with open(p, "r+b") as f:
+        f.truncate(40)
+    assert check8(lib, p)[0] == IO
+
+
 # ---------------- pins of the forward oracle ----------------
 
 def test_rmsnorm_and_swiglu_closed_forms(orc):
@@ -240,3 +305,52 @@ def test_forward_matches_reference_statement(orc):
         assert rel < 1e-2, (step, rel)
         exact += int(np.array_equal(logits, want))
     assert exact >= len(got) // 2, exact
+
+
+def test_e4m3_decode_known_answers_and_round_trip():
+    """The oracle's e4m3 decoder on the reference's known-answer codes
+    (kernel_ops.cpp:1237-1247) and on S.1111.111 (+-480, kernels.h:120-125),
+    and the test quantizer's nearest-even encoding, which must return every
+    finite code from its own value (a wrong exponent bias or mantissa width
+    breaks both)."""
+    from oracle import model_ref as M
+    ka = {0x00: 0.0, 0x66: 56.0, 0xE6: -56.0, 0x7E: 448.0, 0x01: 0.001953125,
+          0x02: 0.00390625, 0x07: 0.013671875, 0x08: 0.015625, 0x40: 2.0, 0x50: 8.0,
+          0x7F: 480.0, 0xFF: -480.0}
+    for code, want in ka.items():
+        assert M.e4m3_to_f32(np.uint8(code)) == np.float32(want), hex(code)
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], dtype=np.uint8)
+    assert np.array_equal(W.f32_to_e4m3(M.e4m3_to_f32(codes)), codes)
+    # ties go to the even code: halfway between 1.0 (0x38) and 1.125 (0x39)
+    assert W.f32_to_e4m3(np.float32(1.0625)) == 0x38
+    assert W.f32_to_e4m3(np.float32(1.1875)) == 0x3A
+    assert W.f32_to_e4m3(np.float32(1000.0)) == 0x7E   # saturates at 448
+
+
+def test_forward_fp8_matches_reference_statement(orc):
+    """FP8 mode against the reference's numpy statement with use_fp8 for the
+    single-token steps (tests/golden/model_forward_small.json "fp8"): the
+    prefill stays bf16, the decode projections and lm_head use the e4m3 codes
+    and row scales of the same weights. Same tokens, every step within
+    relative L2 1e-2, and the FP8 logits differ from the bf16 run (the mode
+    is live)."""
+    import json
+    from oracle import model_ref as M
+    with open(os.path.join(os.path.dirname(__file__), "golden",
+                           "model_forward_small.json")) as f:
+        d = json.load(f)
+    w = W.golden_small_model(d["seed"], d["vocab"], d["layers"])
+    q = W.golden_small_fp8(w, d["layers"])
+    ref = M.ModelRef({k: orc.bf16_to_f32(v) for k, v in w.items()}, d["layers"], fp8=q)
+    got = [(ref.forward(d["prompt"]), ref.last_logits)]
+    for _ in range(len(d["fp8"]["tokens"]) - 1):
+        ref.decode()
+        got.append((ref.next_token, ref.last_logits))
+    for step, (tok, logits) in enumerate(got):
+        want = orc.bf16_to_f32(np.array(d["fp8"]["logits_bf16"][step], dtype=np.uint16))
+        assert tok == d["fp8"]["tokens"][step], step
+        rel = np.linalg.norm(logits - want) / np.linalg.norm(want)
+        assert rel < 1e-2, (step, rel)
+        if step > 0:
+            bf = orc.bf16_to_f32(np.array(d["logits_bf16"][step], dtype=np.uint16))
+            assert not np.array_equal(want, bf), step

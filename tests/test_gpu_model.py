@@ -282,6 +282,122 @@ def test_argmax(lib, orc, dev):
         assert out.cpu().tolist() == [99999, 0], staged
 
 
+# ---------------- FP8 projections ----------------
+
+def fp8_ref(orc, x, q, scale):
+    """float64 reference of bf16(scale * sum e4m3(q) x)."""
+    from oracle import model_ref as R
+    return (np.asarray(x, np.float64) @ R.e4m3_to_f32(q).astype(np.float64).T) * scale
+
+
+def rnd_codes(rng, shape, specials=True):
+    """Random e4m3 codes; with specials, some 0x7F / 0xFF codes (+-480) and
+    subnormals."""
+    q = rng.integers(0, 256, size=shape, dtype=np.uint8)
+    if not specials:
+        q[(q & 0x7F) == 0x7F] ^= 0x01
+    return q
+
+
+def test_fp8_decode_every_code(lib, orc, dev):
+    """Every e4m3 code through the kernel: W row n holds code n at column k0
+    (zeros elsewhere), x is one-hot at k0 and the scale 1, so y[n] is the
+    code's value, which bf16 holds exactly; the codes 0x7F / 0xFF are
+    +-480 (kernels.h:120-148) and the other rows, without such codes, take
+    the hardware conversion."""
+    import torch
+    from oracle import model_ref as R
+    want = orc.f32_to_bf16(R.e4m3_to_f32(np.arange(256, dtype=np.uint8)))
+    want[0x80] = 0  # -0 * 1 summed into an accumulator that starts at +0
+    for K, k0 in ((2048, 0), (2048, 1037), (6144, 6143)):
+        w = np.zeros((256, K), dtype=np.uint8)
+        w[:, k0] = np.arange(256, dtype=np.uint8)
+        x = np.zeros(K, dtype=np.uint16)
+        x[k0] = 0x3F80  # 1.0
+        y = torch.zeros(256, dtype=torch.int16, device=dev)
+        assert lib.mc_model_gemv_fp8(P(to_dev(w, dev)), P(to_dev(np.ones(256, np.float32), dev)),
+                                     P(to_dev(x, dev)), P(y), 256, K, stream()) == 0
+        torch.cuda.synchronize()
+        got = from_dev(y).view(np.uint16)
+        assert np.array_equal(got, want), (K, k0, [(i, hex(a), hex(b)) for i, (a, b) in
+                                                   enumerate(zip(got, want)) if a != b][:8])
+
+
+@pytest.mark.parametrize("N,K,specials", [(2560, 2048, False), (2048, 6144, True),
+                                          (1000, 2048, True), (130560, 2048, False)])
+def test_gemv_fp8(lib, orc, dev, N, K, specials):
+    import torch
+    rng = np.random.default_rng(N + K)
+    q = rnd_codes(rng, (N, K), specials)
+    scale = (rng.random(N, dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+    x = rnd_bf16(orc, rng, (K,), 1.0)
+    y = torch.zeros(N, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemv_fp8(P(to_dev(q, dev)), P(to_dev(scale, dev)), P(to_dev(x, dev)),
+                                 P(y), N, K, stream()) == 0
+    torch.cuda.synchronize()
+    ref = fp8_ref(orc, orc.bf16_to_f32(x)[None], q, scale)[0]
+    ok, st = within_ulp(orc, from_dev(y), ref, ulps=2.0, frac=0.99)
+    assert ok, st
+
+
+@pytest.mark.parametrize("add", [False, True])
+def test_gemv_fp8_prologues(lib, orc, dev, add):
+    """Norm prologue (residual written bit-exactly), norm prologue with the
+    SwiGLU epilogue (== the projection rounded to bf16, then the SwiGLU), and
+    the SwiGLU prologue, against float64 references."""
+    import torch
+    from oracle import model_ref as R
+    rng = np.random.default_rng(77 + add)
+    res = rnd_bf16(orc, rng, (2048,), 2.0)
+    dlt = rnd_bf16(orc, rng, (2048,), 0.5)
+    g = orc.f32_to_bf16(1 + 0.1 * rng.standard_normal(2048, dtype=np.float32))
+    r = R.bf16(orc.bf16_to_f32(res) + (orc.bf16_to_f32(dlt) if add else 0))
+    x = R.rmsnorm(r[None], orc.bf16_to_f32(g))
+    d_res, d_dlt, d_g = to_dev(res, dev), to_dev(dlt, dev), to_dev(g, dev)
+    # norm prologue
+    N = 2560
+    q = rnd_codes(rng, (N, 2048), True)
+    sc = (rng.random(N, dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+    rout = torch.zeros(2048, dtype=torch.int16, device=dev)
+    y = torch.zeros(N, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemv_fp8_resnorm(P(to_dev(q, dev)), P(to_dev(sc, dev)), P(d_res),
+                                         P(d_dlt) if add else None, P(d_g),
+                                         P(rout) if add else None, P(y), N, C.c_float(1e-6),
+                                         stream()) == 0
+    torch.cuda.synchronize()
+    if add:
+        assert np.array_equal(from_dev(rout), orc.f32_to_bf16(r))
+    ok, st = within_ulp(orc, from_dev(y), fp8_ref(orc, x, q, sc)[0], ulps=2.0, frac=0.99)
+    assert ok, st
+    # norm prologue + SwiGLU epilogue
+    I = 1536
+    q2 = rnd_codes(rng, (2 * I, 2048), False)
+    sc2 = (rng.random(2 * I, dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+    y2 = torch.zeros(I, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemv_fp8_resnorm_swiglu(P(to_dev(q2, dev)), P(to_dev(sc2, dev)),
+                                                P(d_res), P(d_dlt) if add else None, P(d_g),
+                                                None, P(y2), I, C.c_float(1e-6), stream()) == 0
+    torch.cuda.synchronize()
+    gu = R.bf16(fp8_ref(orc, x, q2, sc2)[0])
+    ref = R.silu_mul(gu[:I], gu[I:]).astype(np.float64)
+    ok, st = within_ulp(orc, from_dev(y2), ref, ulps=2.0, frac=0.98)
+    assert ok, st
+    # SwiGLU prologue (the down projection's input), K = 6144
+    gate_up = rnd_bf16(orc, rng, (2 * 6144,), 2.0)
+    q3 = rnd_codes(rng, (2048, 6144), True)
+    sc3 = (rng.random(2048, dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+    y3 = torch.zeros(2048, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemv_fp8_swiglu(P(to_dev(q3, dev)), P(to_dev(sc3, dev)),
+                                        P(to_dev(gate_up, dev)), P(y3), 2048, 6144,
+                                        stream()) == 0
+    torch.cuda.synchronize()
+    gg = orc.bf16_to_f32(gate_up)
+    xs = R.silu_mul(gg[:6144], gg[6144:])
+    ok, st = within_ulp(orc, from_dev(y3), fp8_ref(orc, xs[None], q3, sc3)[0], ulps=2.0,
+                        frac=0.99)
+    assert ok, st
+
+
 # ---------------- whole model through the mc_* ABI ----------------
 
 @pytest.fixture(scope="module")
@@ -396,6 +512,112 @@ def test_model_chunked_prefill_equals_split_calls(rt, model_dir):
     assert a.info()["seq_len"] == b.info()["seq_len"] == 9001
     a.close()
     b.close()
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def model_dir8(tmp_path_factory):
+    """model.wpk (bf16, as model_dir) plus model_fp8.wpk: e4m3 codes of
+    normal samples and row scales for the two layer sets and the lm_head
+    (the oracle runs the same codes, so they need not quantize the bf16
+    weights; codes are cut from the fp32 bits — exponent rebiased, mantissa
+    truncated to 3 bits — which is fast and gives weights shaped like real
+    quantized ones)."""
+    d = tmp_path_factory.mktemp("wpk8")
+    secs = W.model_sections(2)
+    blobs = W.random_blobs(1234, 2, scale=1.0)
+    W.write_wpk(os.path.join(d, "model.wpk"), secs, blobs)
+    rng = np.random.default_rng(88)
+    q8 = {}
+    for key, (n, k) in [(f"{nm}.{s}", shape) for s in range(2) for nm, shape in
+                        (("qkv", (W.QKV, W.HIDDEN)), ("o", (W.HIDDEN, W.HIDDEN)),
+                         ("gate_up", (2 * W.INTER, W.HIDDEN)), ("down", (W.HIDDEN, W.INTER)))] + \
+            [("table", (W.VOCAB, W.HIDDEN))]:
+        v = rng.standard_normal((n, k), dtype=np.float32) * np.float32(64.0)
+        u = v.view(np.uint32)
+        e = ((u >> 23) & 0xFF).astype(np.int32) - 120  # e4m3 exponent field
+        mag = np.where(e < 1, 0, np.minimum((e << 3) | ((u >> 20) & 7), 0x7E))
+        codes = (mag | ((u >> 24) & 0x80)).astype(np.uint8)
+        # rows of rms ~ 1/sqrt(K), the bf16 weights' scale
+        scale = np.full(n, 1.0 / (64.0 * np.sqrt(k)), dtype=np.float32)
+        scale *= (1 + 0.2 * rng.random(n)).astype(np.float32)
+        q8[key] = (codes, scale)
+    secs8 = W.fp8_sections(2, lm_head=True)
+    W.write_fp8_wpk(os.path.join(d, "model_fp8.wpk"), secs8, q8)
+    return str(d), W.weights_f32(secs, blobs), W.fp8_weights(secs8, q8)
+
+
+def test_model_fp8_decode_vs_oracle(rt, orc, model_dir8):
+    """precision MC_FP8 (the dual copy): the prefill runs the bf16 weights, each
+    decode the e4m3 projections and lm_head; logits and tokens against the
+    oracle in FP8 mode; graph replay == eager; batch steps keep the bf16
+    weights and equal a BF16 model's bit for bit."""
+    from oracle import model_ref as R
+    path, w, q8 = model_dir8
+    prompt = [7, 70000, 3, 130000, 12, 99]
+    cfg = rt.gen_config(max_new_tokens=16)
+    ref = R.ModelRef(w, 42, fp8=q8)
+    ref.forward(prompt)
+    logits = {}
+    for graphs in (0, 1):
+        m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2,
+                                            enable_cuda_graph=graphs, precision=2))
+        s = rt.Session(m)
+        s.prefill(prompt)
+        if graphs == 0:
+            rel, cos = compare_logits(s.last_logits(), ref.last_logits)
+            assert rel < 2e-2 and cos > 0.999, (rel, cos)
+        lg = []
+        for step in range(3):
+            tok = s.decode_one(cfg)
+            if graphs == 0:
+                if clear_winner(ref.last_logits):
+                    assert tok == ref.next_token, (step, tok, ref.next_token)
+                ref.next_token = tok
+                ref.decode()
+                rel, cos = compare_logits(s.last_logits(), ref.last_logits)
+                print("fp8 decode", step, "rel", rel, "cos", cos)
+                assert rel < 2e-2 and cos > 0.999, (step, rel, cos)
+            lg.append(s.last_logits())
+        logits[graphs] = lg
+        s.close()
+        m.close()
+    for a, b in zip(logits[0], logits[1]):
+        assert np.array_equal(a, b)
+    # batch steps: bf16 weights in both precisions
+    toks = {}
+    for prec in (0, 2):
+        m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2,
+                                            precision=prec))
+        ss = [rt.Session(m) for _ in range(2)]
+        for s_, p_ in zip(ss, (prompt, prompt[:3])):
+            s_.prefill(p_)
+        g = rt.BatchGroup(m, 2, 4096)
+        slots = [g.add(s_) for s_ in ss]
+        toks[prec] = [g.step(slots, [cfg, cfg]) for _ in range(2)]
+        g.close()
+        for s_ in ss:
+            s_.close()
+        m.close()
+    assert toks[0] == toks[2]
+
+
+def test_model_fp8_needs_both_packages(rt, model_dir8, tmp_path):
+    import shutil
+    path, _, _ = model_dir8
+    only_bf16 = tmp_path / "bf16"
+    only_bf16.mkdir()
+    os.symlink(os.path.join(path, "model.wpk"), only_bf16 / "model.wpk")
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(only_bf16), rt.model_options(precision=2))
+    assert e.value.status == 4 and "model_fp8.wpk" in str(e.value)
+    empty = tmp_path / "empty"
+    empty.mkdir()
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(empty), rt.model_options(precision=2))
+    assert e.value.status == 4
+    # a bf16 load ignores model_fp8.wpk
+    m = rt.Model(path, rt.model_options(precision=0))
     m.close()
 
 

@@ -166,3 +166,137 @@ def golden_small_model(seed: int, vocab: int, layers: int):
         w[p + "gate_up"] = mat(2 * INTER, HIDDEN)
         w[p + "down"] = mat(HIDDEN, INTER)
     return w
+
+
+# ---- FP8 package (model_fp8.wpk) ----
+# The reference's FP8 mode reads a second package, model_fp8.wpk, holding the
+# 42 x {qkv, o, gate_up, down} projections (and optionally the lm_head) as
+# dtype-2 sections: e4m3 bytes [N][K] plus fp32 per-row scales at the entry's
+# scale_offset / scale_bytes (weight_loader.cpp:465-620).
+
+def _e4m3_values():
+    """Values of the non-negative finite codes 0x00..0x7E (ascending)."""
+    codes = np.arange(0x7F, dtype=np.int64)
+    e, m = codes >> 3, (codes & 7).astype(np.float64)
+    return np.where(e == 0, m / 8 * 2.0 ** -6, (1 + m / 8) * np.exp2(e - 7))
+
+
+_E4M3_POS = _e4m3_values()
+
+
+def f32_to_e4m3(x) -> np.ndarray:
+    """fp32 -> e4m3 codes: the nearest value among the 127 non-negative
+    finite codes (ties to the even code), magnitudes past 448 saturating to
+    448 (0x7E), sign in bit 7."""
+    x = np.asarray(x, dtype=np.float64)
+    a = np.minimum(np.abs(x), 448.0)
+    hi = np.clip(np.searchsorted(_E4M3_POS, a), 1, 0x7E)
+    lo = hi - 1
+    dl, dh = a - _E4M3_POS[lo], _E4M3_POS[hi] - a
+    pick_hi = (dh < dl) | ((dh == dl) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    return np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)
+
+
+def quantize_rows(w_bf16) -> tuple:
+    """Per-row e4m3 quantization of a bf16 [N][K] matrix: scale[n] =
+    max|row| / 448 (at least 1e-12), codes = e4m3(w / scale)."""
+    w = (np.asarray(w_bf16, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+    scale = np.maximum(np.max(np.abs(w), axis=-1) / np.float32(448.0),
+                       np.float32(1e-12)).astype(np.float32)
+    return f32_to_e4m3(w / scale[:, None]), scale
+
+
+def fp8_sections(layer_sets: int = 2, lm_head: bool = True):
+    """[(name, (N, K), blob key)] of model_fp8.wpk; layer i uses set i % sets."""
+    out = []
+    for i in range(LAYERS):
+        k = i % layer_sets
+        out += [(f"layer{i}.qkv", (QKV, HIDDEN), f"qkv.{k}"),
+                (f"layer{i}.o", (HIDDEN, HIDDEN), f"o.{k}"),
+                (f"layer{i}.gate_up", (2 * INTER, HIDDEN), f"gate_up.{k}"),
+                (f"layer{i}.down", (HIDDEN, INTER), f"down.{k}")]
+    if lm_head:
+        out.append(("lm_head", (VOCAB, HIDDEN), "table"))
+    return out
+
+
+def fp8_blobs(bf16_blobs, layer_sets: int = 2, lm_head: bool = True):
+    """Quantized blobs key -> (codes uint8 [N][K], scales fp32 [N]) of the
+    bf16 blobs of random_blobs / model_sections."""
+    keys = [f"{n}.{k}" for k in range(layer_sets) for n in ("qkv", "o", "gate_up", "down")]
+    if lm_head:
+        keys.append("table")
+    return {key: quantize_rows(bf16_blobs[key]) for key in keys}
+
+
+def write_fp8_wpk(path, sections, blobs, entry_patch=None):
+    """sections: [(name, (N, K), key)]; blobs: key -> (codes, scales) or
+    (data bytes, scale bytes) ints for holes. Data areas are 256-byte aligned,
+    each blob's scales follow its codes."""
+    hdr_bytes = 64 + len(sections) * 132
+    cursor = (hdr_bytes + 255) // 256 * 256
+    data_start = cursor
+    place = {}
+    for _, _, key in sections:
+        if key in place:
+            continue
+        b = blobs[key]
+        nd, ns = (b[0], b[1]) if isinstance(b[0], int) else (b[0].nbytes, b[1].nbytes)
+        place[key] = (cursor, cursor + (nd + 255) // 256 * 256)
+        cursor = place[key][1] + (ns + 255) // 256 * 256
+    with open(path, "wb") as f:
+        f.write(struct.pack("<IHH32sIIQQ", MAGIC, ABI, TARGET_SM, b"\x00" * 32, len(sections),
+                            0, 64, data_start))
+        for i, (name, (n, k), key) in enumerate(sections):
+            d = {"hash": fnv1a64(name), "dtype": 2, "layout": 0, "rank": 2,
+                 "dims": [n, k] + [0] * 6, "offset": place[key][0], "bytes": n * k,
+                 "scale_offset": place[key][1], "scale_bytes": n * 4}
+            if entry_patch is not None:
+                entry_patch(i, d)
+            f.write(struct.pack("<QIII8IQQQQ6Q", d["hash"], d["dtype"], d["layout"], d["rank"],
+                                *d["dims"], d["offset"], d["bytes"], d["scale_offset"],
+                                d["scale_bytes"], *([0] * 6)))
+        for key, (do, so) in place.items():
+            b = blobs[key]
+            if isinstance(b[0], int):
+                continue
+            f.seek(do)
+            f.write(np.ascontiguousarray(b[0], dtype=np.uint8).tobytes())
+            f.seek(so)
+            f.write(np.ascontiguousarray(b[1], dtype=np.float32).tobytes())
+        f.truncate(cursor)
+    return cursor
+
+
+def fp8_weights(sections, blobs):
+    """Section name -> (codes, scales) for oracle/model_ref.ModelRef(fp8=...)."""
+    return {name: blobs[key] for name, _, key in sections}
+
+
+def golden_small_fp8(w, layers: int):
+    """FP8 copies (codes, scales) of the projections and the lm_head of a
+    golden_small_model weight dict."""
+    names = ["lm_head"] + [f"layer{i}.{n}" for i in range(layers)
+                           for n in ("qkv", "o", "gate_up", "down")]
+    return {n: quantize_rows(w[n]) for n in names}
+
+
+def fp8_sparse_blobs(layer_sets: int = 2):
+    """(code bytes, scale bytes) of every fp8_sections blob (a file of holes)."""
+    b = {"table": (VOCAB * HIDDEN, VOCAB * 4)}
+    for k in range(layer_sets):
+        b.update({f"qkv.{k}": (QKV * HIDDEN, QKV * 4), f"o.{k}": (HIDDEN * HIDDEN, HIDDEN * 4),
+                  f"gate_up.{k}": (2 * INTER * HIDDEN, 2 * INTER * 4),
+                  f"down.{k}": (HIDDEN * INTER, HIDDEN * 4)})
+    return b
+
+
+def fp8_arena_bytes(sections) -> int:
+    """Device bytes of the FP8 copies: codes then scales of each section,
+    each 256-byte aligned, in the loader's order (layers, then lm_head)."""
+    c = 0
+    for _, (n, k), _ in sections:
+        c = (c + n * k + 255) // 256 * 256
+        c = (c + n * 4 + 255) // 256 * 256
+    return c
