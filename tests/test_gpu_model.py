@@ -602,6 +602,29 @@ def test_model_fp8_decode_vs_oracle(rt, orc, model_dir8):
     assert toks[0] == toks[2]
 
 
+def test_model_fp8_lm_head_off(rt, model_dir8, monkeypatch):
+    """MC_FP8_LMHEAD_OFF set at load (weight_loader.cpp:549-560): the decode
+    lm_head stays bf16 while the layer projections run e4m3; logits against
+    the oracle in that configuration."""
+    from oracle import model_ref as R
+    path, w, q8 = model_dir8
+    monkeypatch.setenv("MC_FP8_LMHEAD_OFF", "1")
+    m = rt.Model(path, rt.model_options(max_context_tokens=2048, max_sessions=1, precision=2))
+    monkeypatch.delenv("MC_FP8_LMHEAD_OFF")
+    ref = R.ModelRef(w, 42, fp8={k: v for k, v in q8.items() if k != "lm_head"})
+    s = rt.Session(m)
+    prompt = [11, 22, 33]
+    s.prefill(prompt)
+    ref.forward(prompt)
+    tok = s.decode_one(rt.gen_config(max_new_tokens=4))
+    ref.next_token = tok
+    ref.decode()
+    rel, cos = compare_logits(s.last_logits(), ref.last_logits)
+    assert rel < 2e-2 and cos > 0.999, (rel, cos)
+    s.close()
+    m.close()
+
+
 def test_model_fp8_needs_both_packages(rt, model_dir8, tmp_path):
     import shutil
     path, _, _ = model_dir8
