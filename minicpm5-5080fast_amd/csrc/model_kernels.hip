@@ -196,13 +196,16 @@ struct GemvArgs {
 // with block T threads: plain (x rows of stride ldx), SwiGLU of gate|up rows,
 // or residual add + RMSNorm (K = 2048: r = bf16(res_in + addend) stored to
 // res_out by workgroup 0 when not null, x = bf16(r * inv * norm_w); all M
-// rows' sums of squares in one workgroup reduction). The caller
-// synchronizes before reading sx.
-template <uint32_t M, uint32_t PRO, uint32_t K, uint32_t T>
+// rows' sums of squares in one workgroup reduction). All of a thread's row
+// loads are issued first, then issue() (the caller's first weight loads),
+// then the rest: vector loads complete in issue order, so waiting for the
+// rows does not wait for the weights, and the prologue runs under the weight
+// latency. The caller synchronizes before reading sx.
+template <uint32_t M, uint32_t PRO, uint32_t K, uint32_t T, typename Issue>
 __device__ __forceinline__ void stage_rows(const uint16_t* x, uint32_t ldx,
                                            const uint16_t* res_in, const uint16_t* addend,
                                            const uint16_t* norm_w, uint16_t* res_out,
-                                           uint32_t ldr, float eps, uint4* sx) {
+                                           uint32_t ldr, float eps, uint4* sx, Issue issue) {
     constexpr uint32_t NCH = K / 8u;
     static_assert(PRO != kProResnorm || K == 2048u, "the norm prologue covers 2048 dims");
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -212,19 +215,29 @@ __device__ __forceinline__ void stage_rows(const uint16_t* x, uint32_t ldx,
         // all M rows' sums of squares come out of one workgroup barrier.
         constexpr uint32_t IT = (M * 256u + T - 1u) / T;
         __shared__ float s_part[M][4];
-        uint4 v[IT];
+        uint4 v[IT], d[IT], g[IT];
 #pragma unroll
         for (uint32_t it = 0; it < IT; ++it) {
             const uint32_t i = tid + it * T;
             if (i >= M * 256u) break;  // wave-uniform
             const uint32_t m = i >> 8, c = i & 255u;
+            // (unconditional loads keep the compiler's wait counts exact;
+            // without an addend the residual row is read twice and not added)
             v[it] = ld16(res_in + (size_t)m * ldr + 8u * c);
+            d[it] = ld16((addend != nullptr ? addend : res_in) + (size_t)m * ldr + 8u * c);
+            g[it] = ld16(norm_w + 8u * c);
+        }
+        issue();
+#pragma unroll
+        for (uint32_t it = 0; it < IT; ++it) {
+            const uint32_t i = tid + it * T;
+            if (i >= M * 256u) break;  // wave-uniform
+            const uint32_t m = i >> 8, c = i & 255u;
             if (addend != nullptr) {
-                const uint4 d = ld16(addend + (size_t)m * ldr + 8u * c);
-                v[it].x = pack2(lo_f(v[it].x) + lo_f(d.x), hi_f(v[it].x) + hi_f(d.x));
-                v[it].y = pack2(lo_f(v[it].y) + lo_f(d.y), hi_f(v[it].y) + hi_f(d.y));
-                v[it].z = pack2(lo_f(v[it].z) + lo_f(d.z), hi_f(v[it].z) + hi_f(d.z));
-                v[it].w = pack2(lo_f(v[it].w) + lo_f(d.w), hi_f(v[it].w) + hi_f(d.w));
+                v[it].x = pack2(lo_f(v[it].x) + lo_f(d[it].x), hi_f(v[it].x) + hi_f(d[it].x));
+                v[it].y = pack2(lo_f(v[it].y) + lo_f(d[it].y), hi_f(v[it].y) + hi_f(d[it].y));
+                v[it].z = pack2(lo_f(v[it].z) + lo_f(d[it].z), hi_f(v[it].z) + hi_f(d[it].z));
+                v[it].w = pack2(lo_f(v[it].w) + lo_f(d[it].w), hi_f(v[it].w) + hi_f(d[it].w));
             }
             if (res_out != nullptr && blockIdx.x == 0u)
                 *reinterpret_cast<uint4*>(res_out + (size_t)m * ldr + 8u * c) = v[it];
@@ -245,22 +258,36 @@ __device__ __forceinline__ void stage_rows(const uint16_t* x, uint32_t ldx,
             const uint32_t i = tid + it * T;
             if (i >= M * 256u) break;
             const uint32_t m = i >> 8, c = i & 255u;
-            const uint4 g = ld16(norm_w + 8u * c);
             const float tot = ((s_part[m][0] + s_part[m][1]) + s_part[m][2]) + s_part[m][3];
             const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+            const uint4 gw = g[it];
             uint4 o;
-            o.x = pack2(lo_f(v[it].x) * inv * lo_f(g.x), hi_f(v[it].x) * inv * hi_f(g.x));
-            o.y = pack2(lo_f(v[it].y) * inv * lo_f(g.y), hi_f(v[it].y) * inv * hi_f(g.y));
-            o.z = pack2(lo_f(v[it].z) * inv * lo_f(g.z), hi_f(v[it].z) * inv * hi_f(g.z));
-            o.w = pack2(lo_f(v[it].w) * inv * lo_f(g.w), hi_f(v[it].w) * inv * hi_f(g.w));
+            o.x = pack2(lo_f(v[it].x) * inv * lo_f(gw.x), hi_f(v[it].x) * inv * hi_f(gw.x));
+            o.y = pack2(lo_f(v[it].y) * inv * lo_f(gw.y), hi_f(v[it].y) * inv * hi_f(gw.y));
+            o.z = pack2(lo_f(v[it].z) * inv * lo_f(gw.z), hi_f(v[it].z) * inv * hi_f(gw.z));
+            o.w = pack2(lo_f(v[it].w) * inv * lo_f(gw.w), hi_f(v[it].w) * inv * hi_f(gw.w));
             sx[m * NCH + c] = o;
         }
     } else {
-        for (uint32_t i = tid; i < M * NCH; i += T) {
+        constexpr uint32_t IT = (M * NCH + T - 1u) / T;
+        constexpr uint32_t H = PRO == kProSwiglu ? 2u : 1u;  // gate, up
+        uint4 t[IT][H];
+#pragma unroll
+        for (uint32_t it = 0; it < IT; ++it) {
+            const uint32_t i = tid + it * T;
+            if (i >= M * NCH) break;
             const uint32_t m = i / NCH, c = i % NCH;
             const uint16_t* xr = x + (size_t)m * ldx + 8u * c;
-            if constexpr (PRO == kProSwiglu) sx[i] = swiglu8(ld16(xr), ld16(xr + K));
-            else sx[i] = ld16(xr);
+#pragma unroll
+            for (uint32_t h = 0; h < H; ++h) t[it][h] = ld16(xr + h * K);
+        }
+        issue();
+#pragma unroll
+        for (uint32_t it = 0; it < IT; ++it) {
+            const uint32_t i = tid + it * T;
+            if (i >= M * NCH) break;
+            if constexpr (PRO == kProSwiglu) sx[i] = swiglu8(t[it][0], t[it][1]);
+            else sx[i] = t[it][0];
         }
     }
 }
@@ -302,10 +329,12 @@ __global__ void __launch_bounds__(64u * WV) gemv_kernel(const GemvArgs a) {
                                       8u * (lane + 64u * (grp * kG + c)));
     };
     uint4 wc[R][kG];
-    if (active) load(wc, n, g);
-
     stage_rows<M, PRO, K, T>(a.x, a.ldx, a.res_in, a.addend, a.norm_w, a.res_out, a.ldr, a.eps,
-                             sx);
+                             sx, [&] {
+                                 // an inactive wave loads the last row (exact
+                                 // wait counts; the values are never used)
+                                 load(wc, active ? n : a.N - 1u, g);
+                             });
     __syncthreads();
     if (!active) return;  // wave-uniform; no barrier follows
     float acc[R][M];
@@ -464,17 +493,30 @@ __global__ void __launch_bounds__(64u * f8_waves<PRO>()) gemv8_kernel(const Gemv
                 dst[r][c] = ld_stream(reinterpret_cast<const uint16_t*>(
                     a.w + (size_t)(col + r * a.N) * K + 16u * (lane + 64u * c)));
     };
-    // the first row's loads go out before the activation prologue
-    uint4 wc[R][KC8];
-    if (active) load(wc, n);
     // this lane's activation values k = 16 (lane + 64 c) + j, as fp32: with
     // the norm prologue from the row staged once per workgroup in LDS, else
-    // read directly (the SwiGLU applied per lane)
+    // read directly (the SwiGLU applied per lane). The activation loads go
+    // out before the first row's weight loads, so waiting for them does not
+    // wait for the weights (vector loads complete in issue order).
+    uint4 wc[R][KC8];
     __shared__ uint4 sx[PRO == kProResnorm ? K / 8u : 1u];
+    constexpr uint32_t XH = PRO == kProSwiglu ? 2u : 1u;  // gate, up
+    uint4 xraw[PRO == kProResnorm ? 1u : KC8][2][XH];
     if constexpr (PRO == kProResnorm) {
         stage_rows<1u, PRO, K, 64u * kF8Waves>(nullptr, 0u, a.res_in, a.addend, a.norm_w,
-                                               a.res_out, 0u, a.eps, sx);
+                                               a.res_out, 0u, a.eps, sx, [&] {
+                                                   load(wc, active ? n : a.N - 1u);
+                                               });
         __syncthreads();
+    } else {
+#pragma unroll
+        for (uint32_t c = 0; c < KC8; ++c)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h)
+#pragma unroll
+                for (uint32_t e = 0; e < XH; ++e)
+                    xraw[c][h][e] = ld16(a.x + 16u * (lane + 64u * c) + 8u * h + e * K);
+        load(wc, active ? n : a.N - 1u);
     }
     if (!active) return;  // wave-uniform; no barrier follows
     float x[KC8][16];
@@ -485,10 +527,10 @@ __global__ void __launch_bounds__(64u * f8_waves<PRO>()) gemv8_kernel(const Gemv
             uint4 t;
             if constexpr (PRO == kProResnorm) {
                 t = sx[2u * (lane + 64u * c) + h];
+            } else if constexpr (PRO == kProSwiglu) {
+                t = swiglu8(xraw[c][h][0], xraw[c][h][1]);
             } else {
-                const uint16_t* xp = a.x + 16u * (lane + 64u * c) + 8u * h;
-                if constexpr (PRO == kProSwiglu) t = swiglu8(ld16(xp), ld16(xp + K));
-                else t = ld16(xp);
+                t = xraw[c][h][0];
             }
             const uint32_t u[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
