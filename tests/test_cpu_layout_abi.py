@@ -120,3 +120,29 @@ def test_prefill_status_hook_without_gpu(pkg, kvm):
     with pytest.raises(pkg.McError) as e:
         kvm.debug_prefill_status()
     assert e.value.status == 3
+
+
+def test_model_load_option_checks_without_gpu(pkg, tmp_path):
+    """mc_model_load's option checks in the reference's order and codes
+    (native/runtime/model.cpp:58-100, tests/abi_smoke.cpp:118-134): weight
+    and cache precision first (MC_E_UNSUPPORTED), then device_id, sessions
+    and a zero context (MC_E_INVALID_ARGUMENT), then a context beyond the
+    model's 131072 positions (MC_E_UNSUPPORTED); all before any device call."""
+    import importlib
+    rt = importlib.import_module(pkg.__name__ + ".runtime")
+    cases = [
+        (dict(precision=1), 7, "precision"),                    # MC_FP16
+        (dict(precision=3), 7, "precision"),                    # MC_NVFP4
+        (dict(kv_precision=1), 7, "KV cache"),                  # MC_KV_FP8
+        (dict(precision=1, max_sessions=0), 7, "precision"),    # precision first
+        (dict(device_id=-1), 1, "device_id"),
+        (dict(max_sessions=0), 1, "max_sessions"),
+        (dict(max_context_tokens=0), 1, "max_context_tokens"),
+        (dict(max_context_tokens=0, max_sessions=0), 1, "max_sessions"),
+        (dict(max_context_tokens=131073), 7, "131072"),
+        (dict(abi_version=0), 1, "ABI"),
+    ]
+    for kw, status, word in cases:
+        with pytest.raises(pkg.McError) as e:
+            rt.Model(str(tmp_path), rt.model_options(**kw))
+        assert e.value.status == status and word in str(e.value), (kw, e.value)

@@ -84,6 +84,9 @@ def test_model_load_validation(rt, tmp_path):
     assert e.value.status == 2
     with pytest.raises(rt.McError) as e:
         rt.Model(str(tmp_path), rt.model_options(max_context_tokens=0))
+    assert e.value.status == 1
+    with pytest.raises(rt.McError) as e:
+        rt.Model(str(tmp_path), rt.model_options(max_context_tokens=131073))
     assert e.value.status == 7
     (tmp_path / "model.wpk").write_bytes(b"x")  # a package too short for its header
     with pytest.raises(rt.McError) as e:

@@ -638,7 +638,7 @@ def test_model_fp8_needs_both_packages(rt, model_dir8, tmp_path):
     empty.mkdir()
     with pytest.raises(rt.McError) as e:
         rt.Model(str(empty), rt.model_options(precision=2))
-    assert e.value.status == 4
+    assert e.value.status == 4 and "model_fp8.wpk" in str(e.value)  # abi_smoke.cpp:118-127
     # a bf16 load ignores model_fp8.wpk
     m = rt.Model(path, rt.model_options(precision=0))
     m.close()
