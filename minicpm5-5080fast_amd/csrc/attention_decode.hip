@@ -620,11 +620,13 @@ extern "C" mc_status_t mc_kv_debug_decode_timeline(uint64_t* d_stamps, uint32_t 
                   (void*)d_stamps, launches);
         return MC_E_INVALID_ARGUMENT;
     }
+    MC_GUARD_BEGIN
     std::lock_guard<std::mutex> lk(g_tl_mu);
     g_tl_buf = reinterpret_cast<unsigned long long*>(d_stamps);
     g_tl_launches = launches;
     g_tl_next = 0u;
     return MC_OK;
+    MC_GUARD_END
 }
 
 extern "C" mc_status_t mc_kv_debug_decode_records_only(uint32_t enable, uint32_t* previous) {

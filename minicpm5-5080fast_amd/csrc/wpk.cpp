@@ -442,7 +442,9 @@ extern "C" mc_status_t mc_model_wpk_check(const char* path, uint64_t* arena_byte
         mckv::set_error("mc_model_wpk_check: path or arena_bytes is NULL");
         return MC_E_INVALID_ARGUMENT;
     }
+    MC_GUARD_BEGIN
     return mckv::wpk_load(path, nullptr, arena_bytes, nullptr);
+    MC_GUARD_END
 }
 
 extern "C" mc_status_t mc_model_wpk_fp8_check(const char* path, uint64_t* arena_bytes) {
@@ -450,5 +452,7 @@ extern "C" mc_status_t mc_model_wpk_fp8_check(const char* path, uint64_t* arena_
         mckv::set_error("mc_model_wpk_fp8_check: path or arena_bytes is NULL");
         return MC_E_INVALID_ARGUMENT;
     }
+    MC_GUARD_BEGIN
     return mckv::wpk_load_fp8(path, nullptr, arena_bytes, nullptr);
+    MC_GUARD_END
 }
