@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <cstdlib>
 #include <utility>
 
 #include "error.h"
@@ -40,6 +41,16 @@ namespace mckv {
 namespace {
 
 constexpr double kTheta = 5.0e6;  // generated_model_config.h:23
+
+// MC_ROPE_TABLE_OFF (read once per process, forward.cpp:248-262): the RoPE
+// kernel computes its frequencies itself instead of reading the table, and
+// a decode step runs it before the attention instead of the attention's
+// phase0 append (the same values bit for bit: the kernel evaluates the
+// table's own expression, and phase0 equals rope-then-attend).
+bool rope_table_off() {
+    static const bool off = std::getenv("MC_ROPE_TABLE_OFF") != nullptr;
+    return off;
+}
 
 size_t a256(size_t x) { return (x + 255u) & ~size_t(255); }
 
@@ -125,7 +136,7 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
     for (uint32_t l = 0; l < kModelLayers; ++l) {
         FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.qkv[l], kQkvCols, kHidden, f.qkv));
         FWD_OR_RETURN(mc_kv_rope_append(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout, kTheta,
-                                        f.inv_freq, st));
+                                        rope_table_off() ? nullptr : f.inv_freq, st));
         FWD_OR_RETURN(mc_kv_attention_prefill(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
                                               f.attn, S > 1u ? f.pf_partials : nullptr, S, st));
         FWD_OR_RETURN(gemm_bf16(f, f.attn, n, w.o[l], kHidden, kHidden, f.o_out));
@@ -172,8 +183,12 @@ mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_ne
                                                 st));
         if (pending != nullptr) std::swap(cur, other);
         mark();
+        if (rope_table_off())
+            FWD_OR_RETURN(mc_kv_rope_append(f.qkv, 1, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
+                                            kTheta, nullptr, st));
         FWD_OR_RETURN(mc_kv_attention_decode(f.qkv, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
-                                             f.partials, f.max_chunks, f.attn, st, f.inv_freq,
+                                             f.partials, f.max_chunks, f.attn, st,
+                                             rope_table_off() ? nullptr : f.inv_freq,
                                              f.chunk_pos, f.partials2));
         if (q8) {
             FWD_OR_RETURN(mc_model_gemv_fp8(w.q_o[l], w.s_o[l], f.attn, f.o_out, kHidden, kHidden,

@@ -145,13 +145,17 @@ def kv_off(P, maxp, layer, page, slot, kv, head, d) -> int:
     return int(lib().orc_kv_off(P, maxp, layer, page, slot, kv, head, d))
 
 
-def chunk_pos(max_ctx: int) -> int:
-    """native/kernels/sm120/kernels.h:295-304 (512 tier disabled by default)."""
+def chunk_pos(max_ctx: int, c512: bool = False) -> int:
+    """native/kernels/sm120/kernels.h:292-304; c512: MC_ATTN_CHUNK512_ON set
+    (and MC_ATTN_CHUNK512_OFF unset), which gives contexts above 114688
+    positions 512-position chunks."""
     if max_ctx <= 16384:
         return 64
     if max_ctx <= 49152:
         return 128
-    return 256
+    if max_ctx <= 114688 or not c512:
+        return 256
+    return 512
 
 
 def prefill_split_kv(tokens: int) -> int:

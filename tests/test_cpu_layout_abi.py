@@ -146,3 +146,24 @@ def test_model_load_option_checks_without_gpu(pkg, tmp_path):
         with pytest.raises(pkg.McError) as e:
             rt.Model(str(tmp_path), rt.model_options(**kw))
         assert e.value.status == status and word in str(e.value), (kw, e.value)
+
+
+def test_chunk512_tier_from_environment(orc):
+    """MC_ATTN_CHUNK512_ON gives contexts above 114688 positions 512-position
+    chunks, MC_ATTN_CHUNK512_OFF overrides it (kernels.h:292-304); the
+    switches are read once per process, so each case runs in its own."""
+    import subprocess
+    import sys
+    ctxs = (16384, 49152, 114688, 114689, 131072)
+    code = ("import importlib, sys; sys.path.insert(0, %r); "
+            "kvm = importlib.import_module('minicpm5-5080fast_amd').kv; "
+            "print(*[kvm.attention_decode_chunk_pos(c) for c in %r])" % (ROOT, ctxs))
+    for env, c512 in (({"MC_ATTN_CHUNK512_ON": "1"}, True),
+                      ({"MC_ATTN_CHUNK512_ON": "1", "MC_ATTN_CHUNK512_OFF": "1"}, False),
+                      ({"MC_ATTN_CHUNK512_OFF": "1"}, False), ({}, False)):
+        e = {k: v for k, v in os.environ.items() if not k.startswith("MC_ATTN_CHUNK512")}
+        e.update(env)
+        out = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True,
+                             text=True, timeout=120, check=True).stdout.split()
+        assert [int(x) for x in out] == [orc.chunk_pos(c, c512) for c in ctxs], (env, out)
+    assert [orc.chunk_pos(c, True) for c in ctxs] == [64, 128, 256, 512, 512]
