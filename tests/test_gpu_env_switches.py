@@ -8,6 +8,10 @@ environment, each case in a child process of its own:
 * MC_ATTN_CHUNK512_ON (native/kernels/sm120/kernels.h:292-304): a session
   of more than 114688 positions decodes with 512-position chunks; its logits
   are checked against the forward oracle.
+* MC_PREFILL_CHUNK (native/runtime/prefill_executor.cpp:27-50): tokens per
+  prefill forward, 8448..65535; a prompt is prefilled in chunks of that
+  size (bit-identical to mc_prefill calls of the chunk lengths), and an
+  invalid value keeps 8448 with a warning.
 """
 import json
 import os
@@ -49,9 +53,12 @@ m.close()
 """
 
 
+SWITCHES = ("MC_ROPE_TABLE_OFF", "MC_ATTN_CHUNK512_ON", "MC_ATTN_CHUNK512_OFF",
+            "MC_PREFILL_CHUNK")
+
+
 def run_child(path, ctx, graphs, tmp_path, name, env):
-    e = {k: v for k, v in os.environ.items()
-         if k not in ("MC_ROPE_TABLE_OFF", "MC_ATTN_CHUNK512_ON", "MC_ATTN_CHUNK512_OFF")}
+    e = {k: v for k, v in os.environ.items() if k not in SWITCHES}
     e.update(env)
     out = str(tmp_path / (name + ".npy"))
     print("child", name, env, ctx, graphs, flush=True)
@@ -101,3 +108,42 @@ def test_chunk512_session_vs_oracle(model_dir, tmp_path):
         if step < 3:
             ref.next_token = info["tokens"][step]
             ref.decode()
+
+
+# child: one 9552-token prompt prefilled whole and as two mc_prefill calls
+# split at 9000 and at 8448; prints which splits equal the whole bit for bit
+CHILD_PF = r"""
+import importlib, json, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+rt = importlib.import_module("minicpm5-5080fast_amd.runtime")
+m = rt.Model(sys.argv[2], rt.model_options(max_context_tokens=16384, max_sessions=3))
+prompt = [(i * 7919 + 11) % 130560 for i in range(9552)]
+whole = rt.Session(m)
+whole.prefill(prompt)
+res = {}
+for cut in (9000, 8448):
+    s = rt.Session(m)
+    s.prefill(prompt[:cut])
+    s.prefill(prompt[cut:])
+    res[str(cut)] = bool(np.array_equal(whole.last_logits(), s.last_logits()))
+    s.close()
+whole.close()
+m.close()
+print(json.dumps(res))
+"""
+
+
+@pytest.mark.parametrize("value,cut", [("9000", "9000"), (None, "8448"), ("100", "8448")])
+def test_prefill_chunk_from_environment(model_dir, value, cut):
+    path, _ = model_dir
+    e = {k: v for k, v in os.environ.items() if k not in SWITCHES}
+    if value is not None:
+        e["MC_PREFILL_CHUNK"] = value
+    print("child prefill chunk", value, flush=True)
+    r = subprocess.run([sys.executable, "-c", CHILD_PF, ROOT, path], env=e,
+                       capture_output=True, text=True, timeout=100)
+    assert r.returncode == 0, r.stderr[-2000:]
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res[cut], res
+    assert ("MC_PREFILL_CHUNK" in r.stderr) == (value == "100")
