@@ -354,3 +354,45 @@ def test_forward_fp8_matches_reference_statement(orc):
         if step > 0:
             bf = orc.bf16_to_f32(np.array(d["logits_bf16"][step], dtype=np.uint16))
             assert not np.array_equal(want, bf), step
+
+
+def test_mutated_headers_rejected_cleanly(lib, tmp_path):
+    """Random corruptions of a valid package's header and section table (byte
+    flips, 32- and 64-bit fields set to edge values, truncated or extended
+    files) come back as a status with a message, for both package checks;
+    the parser is never driven outside its buffers."""
+    import random
+    import struct
+    W.write_wpk(tmp_path / "b.wpk", W.model_sections(), W.sparse_blobs())
+    W.write_fp8_wpk(tmp_path / "f.wpk", W.fp8_sections(), W.fp8_sparse_blobs())
+    bases = [(open(tmp_path / k, "rb").read(65536), os.path.getsize(tmp_path / k))
+             for k in ("b.wpk", "f.wpk")]
+    rng = random.Random(20261202)
+    edge = [0, 1, 0xFF, 0xFFFF, 0x7FFFFFFF, 0xFFFFFFFF, 1 << 32, 1 << 63, (1 << 64) - 1]
+    seen = set()
+    p = tmp_path / "m.wpk"
+    for _ in range(150):
+        head, size = rng.choice(bases)
+        h = bytearray(head)
+        for _ in range(rng.randint(1, 4)):
+            off = rng.randrange(0, 64 + 132 * 170 - 8)
+            r = rng.random()
+            if r < 0.4:
+                h[off] = rng.randrange(256)
+            elif r < 0.7:
+                struct.pack_into("<I", h, off & ~3, rng.choice(edge) & 0xFFFFFFFF)
+            else:
+                struct.pack_into("<Q", h, off & ~7, rng.choice(edge + [size, size + 1]))
+        sz = rng.choice([size, size, size, rng.randrange(0, 70000), size - 4096])
+        with open(p, "wb") as f:
+            f.write(bytes(h[:min(len(h), sz)]))
+            if sz > len(h):
+                f.truncate(sz)
+        n = C.c_uint64(0)
+        for fn in (lib.mc_model_wpk_check, lib.mc_model_wpk_fp8_check):
+            st = fn(str(p).encode(), C.byref(n))
+            assert st in (OK, IO, MISMATCH, UNSUPPORTED), st
+            if st != OK:
+                assert lib.mc_last_error()
+            seen.add(st)
+    assert MISMATCH in seen
