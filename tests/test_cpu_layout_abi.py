@@ -49,8 +49,12 @@ def test_bad_layout_rejected(pkg):
 
 
 def test_tier_tables(kvm, orc):
+    # the library reads MC_ATTN_CHUNK512_ON / _OFF once per process; the
+    # literals are the default table
+    c512 = "MC_ATTN_CHUNK512_ON" in os.environ and "MC_ATTN_CHUNK512_OFF" not in os.environ
     for ctx, c in GOLD["chunk_pos_tiers"]:
-        assert kvm.attention_decode_chunk_pos(ctx) == c == orc.chunk_pos(ctx)
+        assert kvm.attention_decode_chunk_pos(ctx) == orc.chunk_pos(ctx, c512)
+        assert orc.chunk_pos(ctx) == c
     assert kvm.attention_decode_max_chunks(131072, 256) == 512
     assert kvm.attention_decode_max_chunks(8448, 64) == 132
     for t, s in GOLD["prefill_split_kv"]:
