@@ -152,6 +152,7 @@ struct DecodeArgs {
     bool split;       // record layout per head: false {m, l, acc[128]} rows,
                       // true acc[rec_stride][128] then {m, l}[rec_stride]
     uint16_t* out;    // this slot: [2048]
+    unsigned long long* first_data;  // timeline word for the first tile's arrival, or nullptr
 };
 
 
@@ -574,6 +575,15 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                     if (c + ga / TPW < c_end)
                         clamp_load(R[ga % RING], c + ga / TPW, ga % TPW, false);
                     const uint32_t j = wave + 4u * i;
+                    if (h == 0u && i == 0u && a.first_data != nullptr && c == c_first &&
+                        threadIdx.x < 64u) {
+                        // timeline: clock at which the first tile's K/V are in
+                        // registers (the wait the accumulate below needs anyway)
+                        uint32_t k0 = R[0].k[0].x;
+                        asm volatile("" : "+v"(k0));
+                        if (threadIdx.x == 0u)
+                            *a.first_data = __builtin_amdgcn_s_memrealtime() + (k0 & 0u);
+                    }
                     if (cc2 < c_end && j < chunk_tiles(cc2))
                         accumulate(xpose(R[g % RING]), cc2 * C + j * kTile, chunk_end(cc2));
                 }
@@ -674,7 +684,9 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 
 // Debug timeline (mc_kv_debug_decode_timeline): with a stamp buffer attached,
 // workgroup w of a launch writes, at 4 * w of the launch's chunk region,
-// {entry clock, exit clock, XCC id, 0}: thread 0 stores the entry when the
+// {entry clock, exit clock, XCC id, first data clock}: the last is the clock
+// at which the workgroup's first K/V tile reached registers (straight-line
+// schedule; 0 otherwise); thread 0 stores the entry when the
 // workgroup starts and every wave raises the exit to the clock at which it
 // leaves (a vector atomic max). The clock is s_memrealtime (100 MHz, one
 // count per 10 ns, common to all CUs). Workgroups past kTlChunkWgs are not
@@ -726,7 +738,7 @@ __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
 // batched launches resolve per-slot pointers from device tables. Records of
 // slot s start at partials + s * 16 * rec_stride * 130 with a per-head stride
 // of rec_stride records (rec_stride >= the number of ranges, ceil(NC / cpw)).
-template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P>
+template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P, bool FIXED>
 __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
     __attribute__((amdgpu_waves_per_eu(2))) decode_chunk_kernel(
     const uint16_t* __restrict__ q_rows, const uint32_t* d_pos,
@@ -752,10 +764,21 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
         a.rec_stride = rec_stride;
         a.split = split;
         a.out = out + (size_t)slot * kHq * kD;
+        a.first_data = stamp.p != nullptr ? stamp.p + 3 : nullptr;
         decode_range_body<PH0, PAGE16, TPW, KV2, FP32P>(a, layer, ly, NC, inv_freq, C, kvh,
                                                         group, cpw);
     };
     if constexpr (BATCH) {
+        if constexpr (FIXED) {
+            // Small grids (every workgroup resident at once): workgroup
+            // (slot, head, range) = (x, y, z), so the workgroup knows its slot
+            // without reading every slot's limit first (one dependent load
+            // round and the scan fewer before its first K/V; measured C3
+            // 12.3 against 12.8 us/layer). Slot is the fastest index so the
+            // early ranges of all slots are dispatched first.
+            run(blockIdx.x, blockIdx.z, min(*slot_pos[blockIdx.x], pos_max));
+            return;
+        }
         // Work compaction: the (x, slot) workgroups are numbered densely over
         // the chunk groups that exist (slot by slot, ascending), so ragged
         // slots leave their idle workgroups at the end of the grid instead of
@@ -836,15 +859,32 @@ inline bool use_kv2(const ChunkLaunch& L) {
     return !L.batched && (L.C == 256u || L.C == 512u) && nx >= kKv2MinBlocks;
 }
 
+// Batched grids of at most this many workgroups (two per CU) map workgroups
+// to (slot, range) directly; larger ones, whose ragged slots leave many
+// ranges idle, number the existing ranges densely (a direct mapping was
+// measured 38 -> 111 us/layer at C5, idle workgroups delaying the long
+// sessions' ranges).
+constexpr uint32_t kFixedMapMaxWgs = 512;
+
 template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P>
 void launch_one(const ChunkLaunch& L) {
     const uint32_t nx = (L.NC + L.cpw - 1u) / L.cpw;
-    const dim3 grid(nx, KV2 ? 1u : kHkv, L.B);
+    const uint32_t heads = KV2 ? 1u : kHkv;
+    const bool fixed_map = BATCH && (uint64_t)nx * heads * L.B <= kFixedMapMaxWgs;
     const dim3 block(KV2 ? kHkv * kThreads : kThreads);
-    hipLaunchKernelGGL((decode_chunk_kernel<PH0, BATCH, PAGE16, TPW, KV2, FP32P>), grid, block,
-                       0, L.st, L.q, L.d_pos, L.slot_pos, L.layer, L.pt, L.slot_pt, L.pool,
-                       L.slot_kv, L.ly, L.partials, L.NC, L.rec_stride, L.out, L.inv_freq, L.C,
-                       L.cpw, L.B, L.split, L.stamps);
+#define MC_CHUNK_LAUNCH(FX, GRID)                                                            \
+    hipLaunchKernelGGL((decode_chunk_kernel<PH0, BATCH, PAGE16, TPW, KV2, FP32P, FX>), GRID,  \
+                       block, 0, L.st, L.q, L.d_pos, L.slot_pos, L.layer, L.pt, L.slot_pt,    \
+                       L.pool, L.slot_kv, L.ly, L.partials, L.NC, L.rec_stride, L.out,        \
+                       L.inv_freq, L.C, L.cpw, L.B, L.split, L.stamps)
+    if constexpr (BATCH && !KV2) {
+        if (fixed_map) {
+            MC_CHUNK_LAUNCH(true, dim3(L.B, heads, nx));
+            return;
+        }
+    }
+    MC_CHUNK_LAUNCH(false, dim3(nx, heads, L.B));
+#undef MC_CHUNK_LAUNCH
 }
 
 template <bool PH0, bool BATCH, bool PAGE16, bool FP32P>

@@ -225,8 +225,10 @@ def timeline_summary(stamps) -> dict:
     launches * TIMELINE_WORDS words): the written regions ordered by chunk
     entry, each giving the chunk span (first workgroup entry to last wave
     exit), the median and latest workgroup entry, the per-XCC median exit
-    range, the gap to the merge's first entry, the merge span, and the gap to
-    the next decode's chunk entry. Clock counts are 10 ns; results in us."""
+    range, the medians over workgroups of entry -> first K/V tile in registers
+    and first tile -> exit, the gap to the merge's first entry, the merge
+    span, and the gap to the next decode's chunk entry. Clock counts are
+    10 ns; results in us."""
     import numpy as np
     st = np.asarray(stamps, dtype=np.int64).reshape(-1, TIMELINE_WORDS)
     recs = []
@@ -246,6 +248,10 @@ def timeline_summary(stamps) -> dict:
         row = {"chunk_span": (b - a) / 100, "median_wg_end": (np.median(ck[:, 1]) - a) / 100,
                "last_wg_entry": (ck[:, 0].max() - a) / 100,
                "xcc_median_end": [min(xcc) / 100, max(xcc) / 100], "workgroups": len(ck)}
+        fd = ck[ck[:, 3] > 0]
+        if len(fd):  # workgroup entry -> its first K/V tile in registers -> its exit
+            row["wg_entry_to_first_data"] = float(np.median(fd[:, 3] - fd[:, 0])) / 100
+            row["wg_first_data_to_exit"] = float(np.median(fd[:, 1] - fd[:, 3])) / 100
         end = b
         if len(mg):
             row["gap_to_merge"] = (mg[:, 0].min() - b) / 100
@@ -256,8 +262,9 @@ def timeline_summary(stamps) -> dict:
             row["decode_period"] = (recs[i + 1][0][:, 0].min() - a) / 100
         rows.append(row)
     out = {"decodes": len(rows)}
-    for k in ("chunk_span", "median_wg_end", "last_wg_entry", "gap_to_merge", "merge_span",
-              "gap_to_next", "decode_period"):
+    for k in ("chunk_span", "median_wg_end", "last_wg_entry", "wg_entry_to_first_data",
+              "wg_first_data_to_exit", "gap_to_merge", "merge_span", "gap_to_next",
+              "decode_period"):
         v = [r[k] for r in rows if k in r]
         if v:
             out[k] = round(float(np.median(v)), 3)

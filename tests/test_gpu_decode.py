@@ -614,11 +614,18 @@ def test_decode_timeline_hook(kvm, dev, ctx, C, nc_ctx, chunk_wgs, merge_wgs):
     mg = st[0, 4 * kvm.TIMELINE_CHUNK_WGS:].reshape(-1, 2)
     assert (ck[:chunk_wgs, 0] > 0).all() and not ck[chunk_wgs:].any()
     assert (ck[:chunk_wgs, 1] >= ck[:chunk_wgs, 0]).all()
+    # first K/V tile in registers: between the workgroup's entry and exit
+    # (one per workgroup whose range holds streamed positions 0..ctx-2)
+    cpw = -(-NC // 256) if NC > 256 else 1
+    fd = ck[:chunk_wgs][ck[:chunk_wgs, 3] > 0]
+    assert len(fd) == 2 * -(-(ctx - 1) // (C * cpw))
+    assert (fd[:, 3] >= fd[:, 0]).all() and (fd[:, 3] <= fd[:, 1]).all()
     assert (mg[:merge_wgs, 0] > 0).all() and not mg[merge_wgs:].any()
     assert (mg[:merge_wgs, 1] >= mg[:merge_wgs, 0]).all()
     assert mg[:merge_wgs, 0].min() >= ck[:chunk_wgs, 1].max()
     assert not st[1:].any()
     summ = kvm.timeline_summary(st)
     assert summ["decodes"] == 1 and summ["chunk_span"] > 0 and summ["merge_span"] > 0
+    assert summ["wg_entry_to_first_data"] > 0 and summ["wg_first_data_to_exit"] >= 0
     run_decode(kvm, dev, q, pool, pt, P, maxp, L, layer, ctx - 1, C, NC)
     assert np.array_equal(from_dev(buf, np.int64).reshape(3, -1), st)
