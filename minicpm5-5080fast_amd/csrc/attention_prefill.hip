@@ -121,6 +121,9 @@ __device__ __forceinline__ float max_across_groups(float x) {
 constexpr uint32_t kStep = 64;   // keys per step (32-key steps measured slower)
 constexpr int kNKB = kStep / 16;  // 16-key blocks per step
 constexpr int kNH = kStep / 32;   // 32-key halves per step (one PV MFMA each)
+// Page-id modes of the K/V gather: per row, one page per 64-key step
+// (P >= 64), one page per 32-key half (P = 32).
+constexpr uint32_t kPageRow = 0, kPageStep = 1, kPageHalf = 2;
 constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
 constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (conflict-free tr reads)
 // LDS operand reads issued this many MFMA blocks ahead of their use (software
@@ -129,7 +132,7 @@ constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (confli
 constexpr int kOperandAhead = 8;
 
 // One job = (query tile, kv head, key split), numbered heavy tile first.
-template <bool PAGE_STEP, uint32_t SH>
+template <uint32_t PM, uint32_t SH>
 __device__ __forceinline__ void prefill_job(
     const uint16_t* __restrict__ q_rows, uint32_t T, uint32_t base_pos, uint32_t layer,
     const uint32_t* __restrict__ pt, const uint16_t* __restrict__ pool, DevLayout ly,
@@ -215,16 +218,22 @@ __device__ __forceinline__ void prefill_job(
     };
     // Page ids are fetched one step ahead of the K/V loads that use them, so
     // a gather waits for one memory latency, not two. With P >= kStep a step lies
-    // in one page and its id is read through the scalar path.
+    // in one page, with P = 32 each 32-key half of a step does: their ids are
+    // read through the scalar path (row r lies in half (r mod 2 kPass) / kPass).
     auto page_ids = [&](uint32_t js, uint32_t (&pg)[kStage]) {
-        if constexpr (PAGE_STEP) {
-            const uint32_t pos = js * kStep;
-            const uint32_t id = pos <= key_end
-                                    ? ((const __attribute__((address_space(4))) uint32_t*)(pt))
-                                          [__builtin_amdgcn_readfirstlane(pos >> ly.log2p)]
-                                    : 0u;
+        if constexpr (PM != kPageRow) {
+            uint32_t id[kNH];
 #pragma unroll
-            for (int r = 0; r < kStage; ++r) pg[r] = id;
+            for (int h = 0; h < kNH; ++h) {
+                const uint32_t pos = js * kStep + (PM == kPageHalf ? 32u * (uint32_t)h : 0u);
+                id[h] = (PM == kPageHalf || h == 0) && pos <= key_end
+                            ? ((const __attribute__((address_space(4))) uint32_t*)(pt))
+                                  [__builtin_amdgcn_readfirstlane(pos >> ly.log2p)]
+                            : 0u;
+            }
+#pragma unroll
+            for (int r = 0; r < kStage; ++r)
+                pg[r] = PM == kPageHalf ? id[(r % (kNH * kPass)) / kPass] : id[0];
         } else {
 #pragma unroll
             for (int r = 0; r < kStage; ++r) {
@@ -234,15 +243,21 @@ __device__ __forceinline__ void prefill_job(
         }
     };
     auto gather = [&](uint32_t js, const uint32_t (&pg)[kStage]) {
-        if constexpr (PAGE_STEP) {
-            // The step lies in one page: scalar page base, 32-bit lane offsets,
-            // and no per-lane range test unless the step passes key_end.
-            const uint16_t* pbase = pool + token_base(ly, layer, pg[0], 0u);
+        if constexpr (PM != kPageRow) {
+            // The step (or each 32-key half) lies in one page: scalar page
+            // base, 32-bit lane offsets, and no per-lane range test unless the
+            // step passes key_end.
+            const uint16_t* pbases[kNH];
+#pragma unroll
+            for (int h = 0; h < kNH; ++h)
+                pbases[h] = pool + token_base(ly, layer, pg[PM == kPageHalf ? h * kPass : 0], 0u);
             const uint32_t step0 = js * kStep;
             const bool full = step0 + kStep - 1u <= key_end;  // wave-uniform
 #pragma unroll
             for (int r = 0; r < kStage; ++r) {
                 const uint32_t key = key_of(r);
+                const uint16_t* pbase =
+                    pbases[PM == kPageHalf ? (r % (kNH * kPass)) / kPass : 0];
                 const uint32_t off = ((step0 + key) & ly.pmask) * kSlotElems +
                                      (r >= kNH * kPass ? 256u : 0u) + kvh * kD + kdb * 8u;
                 if (full) {
@@ -575,7 +590,7 @@ __device__ __forceinline__ void prefill_job(
 // once: t = n - 2*slots slots take three of the 3t lightest jobs each
 // (snake order), the others two of the remaining ones (heaviest with
 // lightest). Every job is computed the same way in both modes.
-template <bool PAGE_STEP, uint32_t SH>
+template <uint32_t PM, uint32_t SH>
 __global__ void __launch_bounds__(PfShape<SH>::kThreads)
     __attribute__((amdgpu_waves_per_eu(2))) prefill_attn_kernel(
     const uint16_t* __restrict__ q_rows, uint32_t T,
@@ -606,7 +621,7 @@ __global__ void __launch_bounds__(PfShape<SH>::kThreads)
     }
     for (uint32_t i = 0; i < nj; ++i) {
         if (i > 0u) __syncthreads();  // LDS buffers are reused by the next job
-        prefill_job<PAGE_STEP, SH>(q_rows, T, base_pos, layer, pt, pool, ly, out, partials,
+        prefill_job<PM, SH>(q_rows, T, base_pos, layer, pt, pool, ly, out, partials,
                                       S, jobs[i]);
     }
 }
@@ -723,21 +738,18 @@ extern "C" mc_status_t mc_kv_attention_prefill(const uint16_t* d_q_rows, uint32_
     // resident 32-row workgroup slots: one per CU (LDS-limited)
     const uint32_t slots =
         shape == kRows32 && g_packing.load(std::memory_order_relaxed) ? cus : 0u;
-    const bool page_step = (1u << ly.log2p) >= kStep;
+    const uint32_t P = 1u << ly.log2p;
+    const uint32_t pm = P >= kStep ? kPageStep : P == 32u ? kPageHalf : kPageRow;
+#define MC_PF_PM(SM)                                             \
+    if (pm == kPageStep) MC_PF_LAUNCH(kPageStep, SM);            \
+    else if (pm == kPageHalf) MC_PF_LAUNCH(kPageHalf, SM);       \
+    else MC_PF_LAUNCH(kPageRow, SM);
     switch (shape) {
-        case kRows32:
-            if (page_step) MC_PF_LAUNCH(true, kRows32);
-            else MC_PF_LAUNCH(false, kRows32);
-            break;
-        case kRows16:
-            if (page_step) MC_PF_LAUNCH(true, kRows16);
-            else MC_PF_LAUNCH(false, kRows16);
-            break;
-        default:
-            if (page_step) MC_PF_LAUNCH(true, kHalves16);
-            else MC_PF_LAUNCH(false, kHalves16);
-            break;
+        case kRows32: MC_PF_PM(kRows32) break;
+        case kRows16: MC_PF_PM(kRows16) break;
+        default: MC_PF_PM(kHalves16) break;
     }
+#undef MC_PF_PM
 #undef MC_PF_LAUNCH
     if (S_kv > 1u)
         hipLaunchKernelGGL(prefill_merge_kernel, dim3(tokens * 16u), dim3(128), 0, st,
