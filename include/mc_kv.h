@@ -259,6 +259,24 @@ mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n)
 size_t mc_debug_session_arena_bytes(mc_session_t session);
 uint32_t mc_debug_session_attn_chunk(mc_session_t session);
 
+/* Graph A/B switch (reference session.cpp:636-641): enabled = 0 makes the
+ * session's decode steps run eagerly although graph mode is on; enabled != 0
+ * returns to graph replay, which only takes effect when the model was
+ * loaded with enable_cuda_graph (the graph is captured at the first graph
+ * step). NULL session: no effect. */
+void mc_debug_session_set_graph_enabled(mc_session_t session, int enabled);
+/* Nodes of the session's captured decode-step graph (hipGraphGetNodes;
+ * reference session.cpp:644-647); 0 when none has been captured yet or for a
+ * NULL session. */
+size_t mc_debug_session_graph_nodes(mc_session_t session);
+/* Regression guard of the RoPE frequency table (reference session.cpp:
+ * 668-686): 1 when the session's 64 inv_freq words on the device are
+ * bit-identical to the snapshot taken at mc_session_create, 0 when they were
+ * overwritten, -1 for a NULL session (or no snapshot), -2 on a HIP error.
+ * Call after the last mc_prefill / mc_decode_one / mc_batch_step returned
+ * (they synchronize the session's stream). */
+int mc_debug_session_rope_intact(mc_session_t session);
+
 /* Decode-step breakdown (reference session.cpp:686-723): when MC_BREAKDOWN
  * is set at mc_session_create, every eager mc_decode_one records events at
  * its segment boundaries (a step replayed as a HIP graph records none; the
@@ -310,6 +328,13 @@ mc_status_t mc_kv_debug_prefill_packing(uint32_t enable, uint32_t* previous);
  * waits for work queued on the device's blocking streams. No reference
  * counterpart (the reference's prefill uses workgroup barriers only). */
 mc_status_t mc_kv_debug_prefill_status(uint32_t* barrier_timeouts, uint32_t reset);
+
+/* Sets the current device's half-barrier timeout count to `count` from the
+ * host (no kernel runs): lets a test check that the session prefill path
+ * (mc_prefill, which reads and clears the count after each chunk and returns
+ * MC_E_INTERNAL when it is non-zero) reports a timeout without making any
+ * wait time out. No reference counterpart. */
+mc_status_t mc_kv_debug_prefill_force_timeouts(uint32_t count);
 
 /* Decode P.V precision (process-wide): 0 = P rounded to bf16 before P.V
  * (default, the reference's HMMA path), 1 = fp32 P (the reference's

@@ -73,6 +73,7 @@ _SIGS = {
     "mc_kv_debug_prefill_shape": (C.c_int, [_u32, _P]),
     "mc_kv_debug_prefill_packing": (C.c_int, [_u32, _P]),
     "mc_kv_debug_prefill_status": (C.c_int, [_P, _u32]),
+    "mc_kv_debug_prefill_force_timeouts": (C.c_int, [_u32]),
     "mc_kv_debug_decode_fp32p": (C.c_int, [_u32, _P]),
     "mc_kv_attention_decode_noalloc": (C.c_int, [_P, _P, _u32, _P, _P, LayoutT, _u32, _P, _P,
                                                  _P, _u32]),

@@ -212,6 +212,9 @@ struct SessionImpl {
     uint64_t min_free = ~0ull;
     StepGraph step_graph;
     uint64_t graph_launches = 0;
+    bool graph_off = false;  // mc_debug_session_set_graph_enabled(s, 0)
+    uint32_t rope_snapshot[64] = {};  // inv_freq words at create
+    bool rope_snapshot_valid = false;
     Breakdown bd;
     // with weights
     Forward fwd;
@@ -348,7 +351,7 @@ mc_status_t prefill_chunk(SessionImpl& s, uint32_t base, uint32_t n) {
         // d_state.next_token, the token the first decode returns
         MC_OR_RETURN(forward_prefill(s.fwd, s.d_seq + base, n, &s.d_state->next_token));
         HIP_OR_RETURN(hipStreamSynchronize(st), "mc_prefill: stream sync failed");
-        return MC_OK;
+        return prefill_barrier_check("mc_prefill");
     }
     const uint32_t S = mc_kv_prefill_split_kv(n);
     for (uint32_t l = 0; l < kLayers; ++l) {
@@ -362,7 +365,7 @@ mc_status_t prefill_chunk(SessionImpl& s, uint32_t base, uint32_t n) {
     // The stream still reads h_state.seq_len's copy source asynchronously; keep
     // the host value stable until the caller synchronizes.
     HIP_OR_RETURN(hipStreamSynchronize(st), "mc_prefill: stream sync failed");
-    return MC_OK;
+    return prefill_barrier_check("mc_prefill");
 }
 
 }  // namespace
@@ -537,6 +540,18 @@ mc_status_t mc_session_create(mc_model_t model, mc_session_t* out_session) {
     s->max_chunks = mc_kv_decode_max_chunks(m->max_ctx, s->chunk_pos);
     s->act_rows = std::min(m->max_ctx, prefill_chunk_tokens());
     const size_t pool_b = (size_t)mc_kv_total_elems(s->layout) * 2u;
+    // With weights: the prefill projections' rocBLAS handle gets its device
+    // workspace from the arena, so rocBLAS never allocates after create.
+    size_t blas_ws = 0;
+    if (m->weights) {
+        void* bh = nullptr;
+        const mc_status_t bs = prefill_blas_create(&bh, &blas_ws);
+        s->blas = static_cast<rocblas_handle>(bh);
+        if (bs != MC_OK) {
+            release_session(s);
+            return bs;
+        }
+    }
     const size_t sizes[] = {
         pool_b,
         (size_t)max_pages * 4u,
@@ -549,6 +564,7 @@ mc_status_t mc_session_create(mc_model_t model, mc_session_t* out_session) {
         (size_t)kHq * kSplit2 * kPartial * 4u,
         (size_t)4096u * kHq * kPartial * 4u,  // prefill: T * S_kv <= 4096
         m->weights ? forward_act_bytes(s->act_rows, 1u) : 0u,
+        blas_ws,
     };
     size_t total = 0;
     for (size_t b : sizes) total += align256(b);
@@ -565,8 +581,8 @@ mc_status_t mc_session_create(mc_model_t model, mc_session_t* out_session) {
     }
     s->arena_bytes = total;
     char* p = static_cast<char*>(s->arena);
-    void* bufs[11];
-    for (int i = 0; i < 11; ++i) {
+    void* bufs[12];
+    for (int i = 0; i < 12; ++i) {
         bufs[i] = p;
         p += align256(sizes[i]);
     }
@@ -597,11 +613,8 @@ mc_status_t mc_session_create(mc_model_t model, mc_session_t* out_session) {
         f.pf_partials = s->pf_partials;
         f.max_chunks = s->max_chunks;
         f.chunk_pos = s->chunk_pos;
-        if (rocblas_create_handle(&s->blas) != rocblas_status_success) {
-            s->blas = nullptr;
-            set_error("mc_session_create: rocblas_create_handle failed");
-            rs = MC_E_CUDA;
-        } else {
+        rs = prefill_blas_workspace(s->blas, bufs[11], blas_ws);
+        if (rs == MC_OK) {
             f.blas = s->blas;
             e = hipHostMalloc((void**)&s->h_emit, sizeof(int32_t));
             if (e != hipSuccess) rs = check_hip(e, "mc_session_create: pinned token buffer");
@@ -610,7 +623,12 @@ mc_status_t mc_session_create(mc_model_t model, mc_session_t* out_session) {
     if (rs == MC_OK) {
         e = hipMemsetAsync(s->d_state, 0, sizeof(DevState), s->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+        // create-time snapshot of the RoPE table (mc_debug_session_rope_intact)
+        if (e == hipSuccess)
+            e = hipMemcpy(s->rope_snapshot, s->inv_freq, sizeof(s->rope_snapshot),
+                          hipMemcpyDeviceToHost);
         if (e != hipSuccess) rs = check_hip(e, "mc_session_create: init failed");
+        else s->rope_snapshot_valid = true;
     }
     if (rs != MC_OK) {
         release_session(s);
@@ -756,7 +774,7 @@ mc_status_t mc_decode_one(mc_session_t session, const mc_generation_config_t* co
     hipStream_t st = s->stream;
     MC_OR_RETURN(mc_kv_allocator_ensure_pages_for(s->kv, s->seq_len + 1u, st));
     TraceRange trace_range("mc_decode_one");
-    const bool graph = s->model->use_graphs;
+    const bool graph = s->model->use_graphs && !s->graph_off;
     if (s->model->weights) {
         // returns the token the previous forward predicted; the forward on it
         // (position seq_len) predicts the next one into d_state.next_token
@@ -815,7 +833,7 @@ mc_status_t mc_decode_one(mc_session_t session, const mc_generation_config_t* co
         }
         return MC_OK;
     }));
-    if (s->model->use_graphs) s->graph_launches += 1;
+    if (graph) s->graph_launches += 1;
     s->h_tok = mock_token(s->seq_len, s->rng);
     HIP_OR_RETURN(hipMemcpyAsync(&s->d_state->next_token, &s->h_tok, 4u,
                                  hipMemcpyHostToDevice, st),
@@ -1230,6 +1248,37 @@ size_t mc_debug_session_arena_bytes(mc_session_t session) {
 
 uint32_t mc_debug_session_attn_chunk(mc_session_t session) {
     return session.impl ? session.impl->chunk_pos : 0u;
+}
+
+void mc_debug_session_set_graph_enabled(mc_session_t session, int enabled) {
+    if (session.impl == nullptr) return;
+    session.impl->graph_off = enabled == 0;
+}
+
+size_t mc_debug_session_graph_nodes(mc_session_t session) {
+    SessionImpl* s = session.impl;
+    if (s == nullptr || s->step_graph.graph == nullptr) return 0u;
+    size_t n = 0;
+    if (hipGraphGetNodes(s->step_graph.graph, nullptr, &n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0u;
+    }
+    return n;
+}
+
+int mc_debug_session_rope_intact(mc_session_t session) {
+    SessionImpl* s = session.impl;
+    if (s == nullptr || !s->rope_snapshot_valid || s->inv_freq == nullptr) return -1;
+    if (hipSetDevice(s->model->device_id) != hipSuccess) {
+        (void)hipGetLastError();
+        return -2;
+    }
+    uint32_t cur[64];
+    if (hipMemcpy(cur, s->inv_freq, sizeof(cur), hipMemcpyDeviceToHost) != hipSuccess) {
+        (void)hipGetLastError();
+        return -2;
+    }
+    return std::memcmp(cur, s->rope_snapshot, sizeof(cur)) == 0 ? 1 : 0;
 }
 
 int mc_debug_breakdown_raw_segments(mc_session_t session) {

@@ -227,8 +227,9 @@ __device__ __forceinline__ void prefill_job(
             for (int h = 0; h < kNH; ++h) {
                 const uint32_t pos = js * kStep + (PM == kPageHalf ? 32u * (uint32_t)h : 0u);
                 id[h] = (PM == kPageHalf || h == 0) && pos <= key_end
-                            ? ((const __attribute__((address_space(4))) uint32_t*)(pt))
-                                  [__builtin_amdgcn_readfirstlane(pos >> ly.log2p)]
+                            ? clamp_page(ly, ((const __attribute__((address_space(4))) uint32_t*)(
+                                                 pt))[__builtin_amdgcn_readfirstlane(
+                                                 table_index(ly, pos))])
                             : 0u;
             }
 #pragma unroll
@@ -238,7 +239,7 @@ __device__ __forceinline__ void prefill_job(
 #pragma unroll
             for (int r = 0; r < kStage; ++r) {
                 const uint32_t pos = js * kStep + key_of(r);
-                pg[r] = pos <= key_end ? pt[pos >> ly.log2p] : 0u;
+                pg[r] = pos <= key_end ? clamp_page(ly, pt[table_index(ly, pos)]) : 0u;
             }
         }
     };
@@ -688,6 +689,43 @@ extern "C" mc_status_t mc_kv_debug_prefill_status(uint32_t* barrier_timeouts, ui
     }
     if (e != hipSuccess) {
         set_error("mc_kv_debug_prefill_status: %s", hipGetErrorString(e));
+        return MC_E_CUDA;
+    }
+    return MC_OK;
+}
+
+namespace mckv {
+// Reads and clears the device's half-barrier timeout count after the caller
+// synchronized its prefill work; a non-zero count means some launch's output
+// may be wrong, reported as MC_E_INTERNAL with the count in the message.
+mc_status_t prefill_barrier_check(const char* who) {
+    uint32_t n = 0u;
+    hipError_t e = hipMemcpyFromSymbol(&n, HIP_SYMBOL(g_barrier_timeouts), sizeof(n), 0,
+                                       hipMemcpyDeviceToHost);
+    if (e == hipSuccess && n != 0u) {
+        const uint32_t zero = 0u;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_barrier_timeouts), &zero, sizeof(zero), 0,
+                              hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        set_error("%s: prefill status read failed: %s", who, hipGetErrorString(e));
+        return MC_E_CUDA;
+    }
+    if (n != 0u) {
+        set_error("%s: %u prefill half-barrier wait(s) ran out of their bound; the prefill "
+                  "output is unreliable",
+                  who, n);
+        return MC_E_INTERNAL;
+    }
+    return MC_OK;
+}
+}  // namespace mckv
+
+extern "C" mc_status_t mc_kv_debug_prefill_force_timeouts(uint32_t count) {
+    const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(mckv::g_barrier_timeouts), &count,
+                                           sizeof(count), 0, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        set_error("mc_kv_debug_prefill_force_timeouts: %s", hipGetErrorString(e));
         return MC_E_CUDA;
     }
     return MC_OK;

@@ -142,6 +142,15 @@ __device__ __forceinline__ s16x4 trunc_bf16x4(const f32x4& t) {
     return __builtin_bit_cast(s16x4, r);
 }
 
+// V tile swizzle of token row t (see xpose in decode_range_body).
+__device__ __forceinline__ uint32_t vswz(uint32_t t) { return ((t >> 1) & 3u) * 4u + (t & 1u); }
+// Dim of rows 4g..4g+3 of the P.V block (m, h) (A operand row 4g + i and
+// accumulator row 4g + i hold dim vdim(m, h, g) + i): the 8-byte half read
+// by lane group g is h ^ (g & 1).
+__device__ __forceinline__ uint32_t vdim(uint32_t m, uint32_t h, uint32_t g) {
+    return 32u * m + 8u * g + 4u * (h ^ (g & 1u));
+}
+
 struct DecodeArgs {
     const uint16_t* q_row;  // [2560] of this slot
     uint32_t limit;
@@ -304,12 +313,19 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                          : table_page(t0);
         load_rows(T, t0, chunk_end(c), page_u);
     };
-    // Row-loaded tile -> operand layout (lane (row, group) holds dims
-    // [32m + 8*group, +8) of token row, m < 4) through this wave's LDS tile:
-    // chunk x of token t is stored at slot x ^ t of row t, so both the stores
-    // (16 chunks of 4 rows per instruction) and the operand reads (one chunk
-    // of 16 rows per lane group) spread over all LDS banks. A wave reads only
-    // what it wrote, in order: no barrier is needed.
+    // Row-loaded tile -> operand layout through this wave's LDS tile. A wave
+    // reads only what it wrote, in order: no barrier is needed.
+    //  * K (64-position tier): chunk x of token t at slot x ^ t of row t; the
+    //    operand read (lane (row, group) takes dims [32m + 8*group, +8) of
+    //    token row) touches one chunk of 16 rows per 16 lanes, all banks.
+    //  * V: chunk x of token t at slot x ^ vswz(t), vswz(t) = 4*((t/2)%4) +
+    //    t%2. Every 16-byte store instruction covers whole rows (conflict
+    //    free for any per-row permutation); the 8-byte transposing reads of
+    //    one instruction address tokens 4*grp + j and chunks 4m + a, and with
+    //    this swizzle plus the half choice below the 32 lanes of rows 0..7
+    //    hit 32 distinct 8-byte bank pairs (all 64 banks once; with 32 banks,
+    //    the 16 lanes of rows 0..3 hit 16 distinct pairs). The former x ^ t
+    //    swizzle put 8 rows on 8 slots and one half: a 4-way conflict.
     auto xpose = [&](const Tile& T) -> Tile {
         if constexpr (!VROWS) return T;
         uint4* xs = s_x[wave];
@@ -317,27 +333,30 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         for (int r = 0; r < 4; ++r) {
             const uint32_t t = grp + 4u * r;
             if constexpr (ROWS) xs[t * 16u + (tok ^ t)] = T.k[r];
-            xs[256u + t * 16u + (tok ^ t)] = T.v[r];
+            xs[256u + t * 16u + (tok ^ vswz(t))] = T.v[r];
         }
         __builtin_amdgcn_wave_barrier();
         Tile O;
         // V^T operands with the transposing LDS read: within each 16-lane
         // group, ds_read_b64_tr_b16 gives lane x the element x%4 of the 8-byte
         // rows addressed by lanes 4j + x/4 (j < 4). Lane 4j + a of group grp
-        // addresses token 4*grp + j, dims 32m + 8a + 4h, so lane x receives
-        // dim 32m + 8(x/4) + 4h + x%4 of tokens 4*grp + j: the A operand of
-        // O^T += V^T x P^T with the same dim order the accumulator uses.
+        // addresses token 4*grp + j, chunk 4m + a, half h ^ (a & 1), so lane
+        // x receives dim vdim(m, h, x/4) + x%4 of tokens 4*grp + j: the A
+        // operand of O^T += V^T x P^T, row x of block (m, h) being dim
+        // vdim(m, h, x/4) + x%4 (the accumulator rows follow the same map).
         const uint32_t vt_tok = 4u * grp + (tok >> 2);
+        const uint32_t a4 = tok & 3u;
         const uint16_t* vs = reinterpret_cast<const uint16_t*>(xs + 256u) + vt_tok * 128u;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const uint32_t x = (4u * m + grp) ^ tok;
             O.k[m] = ROWS ? xs[tok * 16u + x] : T.k[m];
-            const uint16_t* vr = vs + (((4u * m + (tok & 3u)) ^ vt_tok) * 8u);
+            const uint16_t* vr = vs + (((4u * m + a4) ^ vswz(vt_tok)) * 8u);
+            const uint32_t h0 = (a4 & 1u) * 4u;  // element offset of half 0
             const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) s16x4*)(vr));
+                (__attribute__((address_space(3))) s16x4*)(vr + h0));
             const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) s16x4*)(vr + 4));
+                (__attribute__((address_space(3))) s16x4*)(vr + (4u - h0)));
             const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
             O.v[m] = make_uint4(l2.x, l2.y, h2.x, h2.y);
         }
@@ -614,7 +633,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                 uint32_t w[2];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const uint32_t d = 32u * m + 8u * (tok >> 2) + 4u * h + (tok & 3u);
+                    const uint32_t d = vdim(m, h, tok >> 2) + (tok & 3u);
                     w[h] = (uint32_t)s_fresh[128u + d] * 0x10001u;
                 }
                 F.v[m] = make_uint4(w[0], w[0], w[1], w[1]);
@@ -636,7 +655,8 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                *reinterpret_cast<f32x4*>(&s_acc[wave][tok][32u * m + 8u * grp + 4u * h]) =
+                *reinterpret_cast<f32x4*>(
+                    &s_acc[wave][tok][VROWS ? vdim(m, h, grp) : 32u * m + 8u * grp + 4u * h]) =
                     acc[m][h];
     }
     __syncthreads();

@@ -28,8 +28,11 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <utility>
+#include <vector>
 
 #include "error.h"
 #include "kv_common.h"
@@ -84,7 +87,35 @@ mc_status_t gemm_bf16(const Forward& f, const uint16_t* x, uint32_t M, const uin
     return MC_OK;
 }
 
+// Device workspace handed to the prefill projections' rocBLAS handle. With a
+// caller-owned workspace rocBLAS only selects GEMM solutions whose scratch
+// fits in it and never allocates on its own.
+constexpr size_t kBlasWorkspace = size_t(32) << 20;
+
 }  // namespace
+
+mc_status_t prefill_blas_create(void** out, size_t* ws_bytes) {
+    *out = nullptr;
+    *ws_bytes = kBlasWorkspace;
+    rocblas_handle h = nullptr;
+    if (rocblas_create_handle(&h) != rocblas_status_success) {
+        set_error("mc_session_create: rocblas_create_handle failed");
+        return MC_E_CUDA;
+    }
+    *out = h;
+    return MC_OK;
+}
+
+mc_status_t prefill_blas_workspace(void* hv, void* ws, size_t ws_bytes) {
+    rocblas_handle h = static_cast<rocblas_handle>(hv);
+    const rocblas_status st = rocblas_set_workspace(h, ws, ws_bytes);
+    if (st != rocblas_status_success) {
+        set_error("mc_session_create: rocblas_set_workspace failed: %s",
+                  rocblas_status_to_string(st));
+        return MC_E_CUDA;
+    }
+    return MC_OK;
+}
 
 size_t forward_act_bytes(uint32_t rows, uint32_t logit_rows) {
     const size_t r = rows;
@@ -129,6 +160,11 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
         set_error("forward_prefill: %u rows for buffers of %u", n, f.rows);
         return MC_E_INTERNAL;
     }
+    // A one-token chunk is a T = 1 forward, which the reference runs through
+    // its decode path (GEMV projections, FP8 ones in FP8 mode, the phase-0
+    // decode attention and the FP8 lm_head: forward.cpp:117-130,252-282,
+    // 444-456), not through the GEMMs and prefill attention.
+    if (n == 1u) return forward_decode(f, d_ids, d_next, Marker{});
     uint16_t* res = f.res_a;
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, res, kHidden, n, st));
     FWD_OR_RETURN(mc_model_rmsnorm_rows(res, nullptr, w.norm1[0], f.normed, n, kHidden, kRmsEps, st));

@@ -34,6 +34,17 @@ struct DevLayout {
     uint32_t num_layers;
 };
 
+// Page-table index of position pos and a page id read from the table, both
+// clamped to the pool's max_pages (a corrupt table entry or position then
+// addresses a wrong page of the pool instead of memory outside it).
+__host__ __device__ __forceinline__ uint32_t table_index(const DevLayout& ly, uint32_t pos) {
+    const uint32_t i = pos >> ly.log2p;
+    return i < ly.max_pages ? i : ly.max_pages - 1u;
+}
+__host__ __device__ __forceinline__ uint32_t clamp_page(const DevLayout& ly, uint32_t page) {
+    return page < ly.max_pages ? page : ly.max_pages - 1u;
+}
+
 // Element offset of (layer, page, slot) token row (kv=0, head=0, d=0).
 __host__ __device__ __forceinline__ uint64_t token_base(const DevLayout& ly,
                                                         uint32_t layer,

@@ -21,4 +21,9 @@ mc_status_t launch_synth_qkv_batch(uint16_t* rows, uint32_t n,
                                    const uint32_t* const* slot_pos, uint32_t layer,
                                    hipStream_t st);
 
+// Prefill half-barrier status (attention_prefill.hip): after the caller's
+// prefill work has been synchronized, reads and clears the device's timeout
+// count; MC_E_INTERNAL (with a message) when it is non-zero.
+mc_status_t prefill_barrier_check(const char* who);
+
 }  // namespace mckv

@@ -92,6 +92,13 @@ struct Forward {
 size_t forward_act_bytes(uint32_t rows, uint32_t logit_rows);
 void forward_carve(Forward& f, char* base, uint32_t rows, uint32_t logit_rows);
 
+// rocBLAS handle of a session's prefill projections and the size of the
+// device workspace it is to be given (*ws_bytes); prefill_blas_workspace then
+// hands it that much caller memory (carved from the session arena), after
+// which rocBLAS allocates nothing. On failure *h is null.
+mc_status_t prefill_blas_create(void** h, size_t* ws_bytes);
+mc_status_t prefill_blas_workspace(void* h, void* ws, size_t ws_bytes);
+
 // Prefill of n <= rows tokens at positions *d_seq_len.. (ids on the device):
 // K/V of every layer appended, the greedy next token written to *d_next.
 mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, int32_t* d_next);

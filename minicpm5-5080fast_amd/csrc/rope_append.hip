@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(256) rope_append_kernel(
 #pragma unroll
         for (int b = 0; b < 5; ++b) v[b] = ld_stream(row + 512u * b + 8u * lane);
     }
-    uint32_t page = ((scalar_u32p)page_table)[(base + t) >> ly.log2p];
+    uint32_t page = clamp_page(ly, ((scalar_u32p)page_table)[table_index(ly, base + t)]);
     while (true) {
         const uint32_t tn = t + W;
         const bool more = tn < tokens;
@@ -95,7 +95,7 @@ __global__ void __launch_bounds__(256) rope_append_kernel(
             const uint16_t* rown = qkv + (size_t)tn * kRow;
 #pragma unroll
             for (int b = 0; b < 5; ++b) vn[b] = ld_stream(rown + 512u * b + 8u * lane);
-            page_n = ((scalar_u32p)page_table)[(base + tn) >> ly.log2p];
+            page_n = clamp_page(ly, ((scalar_u32p)page_table)[table_index(ly, base + tn)]);
         }
         const uint32_t pos = base + t;
         {  // (cos, sin) of pair `lane`, shared through this wave's LDS row

@@ -186,6 +186,12 @@ def debug_prefill_status(reset: bool = False) -> int:
     return n.value
 
 
+def debug_prefill_force_timeouts(count: int) -> None:
+    """Sets the device's half-barrier timeout count from the host (no kernel
+    runs), so that a test can see the session prefill path report it."""
+    check(lib().mc_kv_debug_prefill_force_timeouts(count), "debug_prefill_force_timeouts")
+
+
 DECODE_FP32P_FROM_ENV = 0xFFFFFFFF
 
 

@@ -80,6 +80,9 @@ def _bind():
         "mc_debug_session_seq": (C.c_int, [Handle, C.POINTER(C.c_int32), C.c_uint32]),
         "mc_debug_session_arena_bytes": (C.c_size_t, [Handle]),
         "mc_debug_session_attn_chunk": (C.c_uint32, [Handle]),
+        "mc_debug_session_set_graph_enabled": (None, [Handle, C.c_int]),
+        "mc_debug_session_graph_nodes": (C.c_size_t, [Handle]),
+        "mc_debug_session_rope_intact": (C.c_int, [Handle]),
         "mc_debug_breakdown_raw_segments": (C.c_int, [Handle]),
         "mc_debug_breakdown_collect": (C.c_int, [Handle, C.POINTER(C.c_double), C.c_int]),
         "mc_debug_batch_group_stats": (C.c_int, [Handle, C.POINTER(C.c_uint64),
@@ -166,6 +169,22 @@ class Session:
 
     def attn_chunk(self) -> int:
         return int(_bind().mc_debug_session_attn_chunk(self.h))
+
+    def set_graph_enabled(self, enabled: bool) -> None:
+        """Graph A/B switch: False runs decode steps eagerly although the
+        model was loaded with graphs on (session.cpp:636-641)."""
+        _bind().mc_debug_session_set_graph_enabled(self.h, 1 if enabled else 0)
+
+    def graph_nodes(self) -> int:
+        """Nodes of the captured decode-step graph (0 before the first graph
+        step)."""
+        return int(_bind().mc_debug_session_graph_nodes(self.h))
+
+    def rope_intact(self) -> int:
+        """1 when the RoPE table equals its create-time snapshot, 0 when it
+        was overwritten, -1 without a session/snapshot, -2 on a HIP error
+        (session.cpp:668-686)."""
+        return int(_bind().mc_debug_session_rope_intact(self.h))
 
     def last_logits(self):
         """bf16 logits (as float32 numpy) of the session's last forward (a

@@ -438,3 +438,72 @@ def test_breakdown_and_group_stats(rt, tmp_path, graphs, monkeypatch):
     s.close()
     plain.close()
     m.close()
+
+
+def test_session_graph_and_rope_hooks(rt, tmp_path):
+    """Debug hooks of session.cpp:636-686: the graph A/B switch gives the same
+    tokens and pool bytes with the graph on and off, the captured graph
+    reports its nodes (> 0 after the first graph step, 0 before), and the RoPE
+    table stays bit-identical to its create-time snapshot through prefill,
+    graph and eager decode and batch steps (sampling_regression.cpp:207-247)."""
+    m = rt.Model(str(tmp_path), rt.model_options(max_context_tokens=2048, max_sessions=4,
+                                                 enable_cuda_graph=1))
+    rng = np.random.default_rng(11)
+    prompt = [int(x) for x in rng.integers(0, 130560, 150)]
+    a, b = rt.Session(m), rt.Session(m)
+    assert a.rope_intact() == 1 and a.graph_nodes() == 0
+    a.prefill(prompt)
+    b.prefill(prompt)
+    assert a.rope_intact() == 1
+    cfg = rt.gen_config(max_new_tokens=100, seed=9)
+    b.set_graph_enabled(False)
+    ta, tb = [], []
+    for i in range(6):
+        if i == 3:  # switch both sessions midway: a to eager, b back to graphs
+            a.set_graph_enabled(False)
+            b.set_graph_enabled(True)
+        ta.append(a.decode_one(cfg))
+        tb.append(b.decode_one(cfg))
+        assert a.rope_intact() == 1 and b.rope_intact() == 1
+    assert ta == tb
+    assert a.graph_nodes() > 0 and b.graph_nodes() == a.graph_nodes()
+    assert a.stats().cuda_graph_launches == 3 and b.stats().cuda_graph_launches == 3
+    for s_ in (a, b):
+        info = s_.info()
+        assert info["seq_len"] == 156
+    pa, pb = a.info(), b.info()
+    nb = pa["pages_owned"] * P * 1024
+    lay = pa["layout"]
+    for layer in (0, 41):
+        off = layer * lay.max_pages * P * 1024
+        assert np.array_equal(d2h(pa["d_pool"] + off, nb, np.uint16),
+                              d2h(pb["d_pool"] + off, nb, np.uint16))
+    g = rt.BatchGroup(m, 2, 2048)
+    slots = [g.add(a), g.add(b)]
+    for _ in range(2):
+        g.step(slots, [cfg, cfg])
+    for sl in slots:
+        g.remove(sl)
+    assert a.rope_intact() == 1 and b.rope_intact() == 1
+    g.close()
+    a.close()
+    b.close()
+    m.close()
+
+
+def test_prefill_barrier_timeout_reported(rt, kvm, model):
+    """A half-barrier timeout count left on the device after a prefill chunk
+    makes mc_prefill fail with MC_E_INTERNAL (instead of returning MC_OK with
+    unreliable rows) and clears the count; the next prefill succeeds. The
+    count is set from the host: no wait is made to time out."""
+    s = rt.Session(model)
+    kvm.debug_prefill_status(reset=True)
+    kvm.debug_prefill_force_timeouts(3)
+    with pytest.raises(rt.McError) as e:
+        s.prefill([1, 2, 3, 4])
+    assert e.value.status == 100 and "half-barrier" in str(e.value)
+    assert kvm.debug_prefill_status() == 0
+    s.reset()
+    s.prefill([1, 2, 3, 4])
+    assert s.info()["seq_len"] == 4
+    s.close()

@@ -515,6 +515,37 @@ def test_model_chunked_prefill_equals_split_calls(rt, model_dir):
     m.close()
 
 
+def test_model_prefill_allocates_nothing_after_create(rt, model_dir):
+    """The session's rocBLAS handle works in a workspace carved from the
+    session arena at create (sized by rocBLAS's own query), so prefills of
+    any length, decodes and resets leave the device's free memory unchanged
+    (memory_arena.h:1-8: no allocation after steady state)."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+
+    def free_bytes():
+        f, t = C.c_size_t(), C.c_size_t()
+        assert hip.hipMemGetInfo(C.byref(f), C.byref(t)) == 0
+        return f.value
+
+    path, _ = model_dir
+    m = rt.Model(path, rt.model_options(max_context_tokens=16384, max_sessions=2))
+    s = rt.Session(m)
+    before = free_bytes()
+    cfg = rt.gen_config(max_new_tokens=64)
+    for n in (1, 7, 100, 333, 2048, 4097, 8448):
+        s.reset()
+        s.prefill([(i * 31 + n) % 130560 for i in range(n)])
+        s.decode_one(cfg)
+        assert free_bytes() == before, n
+    s.reset()
+    s.prefill([(i * 17) % 130560 for i in range(9000)])  # two chunks: 8448 + 552
+    assert free_bytes() == before
+    s.close()
+    m.close()
+
+
 @pytest.fixture(scope="module")
 def model_dir8(tmp_path_factory):
     """model.wpk (bf16, as model_dir) plus model_fp8.wpk: e4m3 codes of
@@ -600,6 +631,53 @@ def test_model_fp8_decode_vs_oracle(rt, orc, model_dir8):
             s_.close()
         m.close()
     assert toks[0] == toks[2]
+
+
+def test_model_one_token_chunk_is_a_decode_forward(rt, orc, model_dir8):
+    """A prefill chunk of one token is a T = 1 forward, which the reference
+    runs through its decode path (forward.cpp:117-130,252-282,444-456): in
+    FP8 mode that means the e4m3 projections and lm_head. A one-token prompt
+    matches the oracle in FP8 mode (and not the bf16 oracle as closely); a
+    prompt whose last chunk is one token (8449 = 8448 + 1) gives the same
+    logits and tokens as two prefill calls of 8448 and 1 tokens, and its last
+    chunk used the FP8 weights (the logits differ from a bf16 model's)."""
+    from oracle import model_ref as R
+    path, w, q8 = model_dir8
+    m = rt.Model(path, rt.model_options(max_context_tokens=16384, max_sessions=2,
+                                        precision=2))
+    s = rt.Session(m)
+    ref = R.ModelRef(w, 42, fp8=q8)
+    s.prefill([4242])
+    ref.forward([4242])
+    rel, cos = compare_logits(s.last_logits(), ref.last_logits)
+    assert rel < 2e-2 and cos > 0.999, (rel, cos)
+    ref_bf16 = R.ModelRef(w, 42)
+    ref_bf16.forward([4242])
+    rel16, _ = compare_logits(s.last_logits(), ref_bf16.last_logits)
+    assert rel16 > 2 * rel, (rel16, rel)  # the FP8 weights were used
+    s.close()
+    prompt = [(i * 7919 + 5) % 130560 for i in range(8449)]
+    a, b = rt.Session(m), rt.Session(m)
+    a.prefill(prompt)
+    b.prefill(prompt[:8448])
+    b.prefill(prompt[8448:])
+    cfg = rt.gen_config(max_new_tokens=8)
+    fp8_logits = a.last_logits()
+    assert np.array_equal(fp8_logits, b.last_logits())
+    assert a.decode_one(cfg) == b.decode_one(cfg)
+    assert np.array_equal(a.last_logits(), b.last_logits())
+    for s_ in (a, b):
+        s_.close()
+    m.close()
+    # precision bf16: the same prompt's last (one-token) chunk runs bf16 GEMVs,
+    # so its logits differ from the FP8 run's (before the T = 1 routing both
+    # ran the bf16 GEMMs and were equal)
+    m = rt.Model(path, rt.model_options(max_context_tokens=16384, max_sessions=1))
+    a = rt.Session(m)
+    a.prefill(prompt)
+    assert not np.array_equal(a.last_logits(), fp8_logits)
+    a.close()
+    m.close()
 
 
 def test_model_fp8_lm_head_off(rt, model_dir8, monkeypatch):
