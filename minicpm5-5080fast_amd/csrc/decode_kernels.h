@@ -116,10 +116,25 @@ constexpr uint32_t kRing = 2;
 // K/V rows are read once per launch: non-temporal loads keep them from
 // displacing cached data (page tables, records) on their way through
 // (C4 30.8 -> 30.0, C3 13.5 -> 12.6, C1 8.35 -> 7.9 us/layer).
+// Pool and page-table pointers of batched launches are loaded from the slot
+// tables, so the compiler cannot tell they address global memory and would
+// emit FLAT accesses, which count against the LDS wait counter as well: every
+// LDS wait of the V transpose would then also wait for the next tile's loads
+// in flight. All of them point into device global memory; the casts below
+// make the accesses global_load / global_store.
+#define MCKV_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const MCKV_GLOBAL T* gptr(const T* p) {
+    return (const MCKV_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ MCKV_GLOBAL T* gptr(T* p) {
+    return (MCKV_GLOBAL T*)p;
+}
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
-    return __builtin_bit_cast(uint4,
-                              __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+    return __builtin_bit_cast(
+        uint4, __builtin_nontemporal_load(reinterpret_cast<const MCKV_GLOBAL u32x4_t*>(gptr(p))));
 }
 
 struct Tile {
@@ -245,7 +260,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t p = min(t0 + grp + 4u * r, cend);
-                const uint32_t page = PAGE16 ? page_u : min(pt[p >> ly.log2p], page_max);
+                const uint32_t page = PAGE16 ? page_u : min(gptr(pt)[p >> ly.log2p], page_max);
                 const uint16_t* src =
                     pool + token_base(ly, layer, page, p & ly.pmask) + kvh * kD + 8u * tok;
                 T.k[r] = ld16(src);
@@ -254,7 +269,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             return;
         }
         const uint32_t p = min(t0 + tok, cend);
-        const uint32_t page = PAGE16 ? page_u : min(pt[p >> ly.log2p], page_max);
+        const uint32_t page = PAGE16 ? page_u : min(gptr(pt)[p >> ly.log2p], page_max);
         const uint16_t* src = pool + token_base(ly, layer, page, p & ly.pmask) + kvcol;
         if constexpr (VROWS) {  // K in operand layout, V as row loads
 #pragma unroll
@@ -262,7 +277,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t pr = min(t0 + grp + 4u * r, cend);
-                const uint32_t pg = PAGE16 ? page : min(pt[pr >> ly.log2p], page_max);
+                const uint32_t pg = PAGE16 ? page : min(gptr(pt)[pr >> ly.log2p], page_max);
                 T.v[r] = ld16(pool + token_base(ly, layer, pg, pr & ly.pmask) + 256u +
                               kvh * kD + 8u * tok);
             }
@@ -432,10 +447,12 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     } else if (owner) {  // K|V of `limit` from the pool, 32 lanes per half
         const uint16_t* src =
             pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
-        fresh_kv = *reinterpret_cast<const uint2*>(src + 256u * (t64 >> 5) + (t64 & 31u) * 4u);
+        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+        fresh_kv = __builtin_bit_cast(uint2, *reinterpret_cast<const MCKV_GLOBAL u32x2_t*>(
+                                                 gptr(src + 256u * (t64 >> 5) + (t64 & 31u) * 4u)));
     }
     uint32_t staged_page = 0u;
-    if (cached_pages) staged_page = min(pt[page0 + min(tid, npages_rng - 1u)], page_max);
+    if (cached_pages) staged_page = min(gptr(pt)[page0 + min(tid, npages_rng - 1u)], page_max);
 
     Tile& A = R[0];
     Tile& B = R[RING > 1u ? 1u : 0u];
@@ -470,11 +487,11 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
             s_fresh[tid] = lo;
             s_fresh[tid + 64u] = hi;
             *reinterpret_cast<uint32_t*>(&s_fresh[128u + 2u * tid]) = fresh_v;
-            uint16_t* dst =
-                pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
+            MCKV_GLOBAL uint16_t* dst =
+                gptr(pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD);
             dst[tid] = lo;
             dst[tid + 64u] = hi;
-            *reinterpret_cast<uint32_t*>(dst + 256u + 2u * tid) = fresh_v;
+            *reinterpret_cast<MCKV_GLOBAL uint32_t*>(dst + 256u + 2u * tid) = fresh_v;
         }
     } else if (owner && tid < 64u) {
         const uint32_t h = tid >> 5, d = (tid & 31u) * 4u;
