@@ -55,6 +55,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "error.h"
 #include "kv_common.h"
@@ -177,6 +178,9 @@ struct DecodeArgs {
                       // true acc[rec_stride][128] then {m, l}[rec_stride]
     uint16_t* out;    // this slot: [2048]
     unsigned long long* first_data;  // timeline word for the first tile's arrival, or nullptr
+    const uint32_t* limit_src;  // the limit's device word, read by the body when the
+                                // body's LSRC is set (else `limit` holds the limit)
+    uint32_t pos_max;           // limits are clamped to this (the pool's last position)
 };
 
 
@@ -193,10 +197,10 @@ struct DecodeArgs {
 // the reference's chunk kernel); the next tile's loads are issued before the
 // current tile computes, also across chunk boundaries. cpw > 1 requires
 // C % 64 == 0.
-template <bool PH0, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P>
+template <bool PH0, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P, bool LSRC>
 __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t layer,
                                                   DevLayout ly, uint32_t NC,
-                                                  const float* __restrict__ inv_freq,
+                                                  const float* inv_freq,
                                                   uint32_t C, uint32_t kvh, uint32_t group,
                                                   uint32_t cpw) {
     constexpr uint32_t NH = KV2 ? 2u : 1u;  // kv heads per workgroup
@@ -232,8 +236,11 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     const uint32_t tok = lane & 15u;  // row within a 16-position tile / head col
     const uint32_t grp = lane >> 4;   // 0..3
 
-    const uint16_t* __restrict__ q_row = a.q_row;
-    const uint32_t* __restrict__ pt = a.pt;
+    // q_row, inv_freq and pt are not restrict-qualified: loads through them
+    // then count as ordinary memory reads, which the start-up's memory
+    // clobbers keep in their round (invariant loads may be sunk past them).
+    const uint16_t* q_row = a.q_row;
+    const uint32_t* pt = a.pt;
     uint16_t* __restrict__ pool = a.pool;
     const uint32_t kvcol = kvh * kD + 8u * grp;  // within a token's K or V half
     // Page ids are clamped to the pool and table indices to the table's
@@ -293,7 +300,69 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     constexpr uint32_t RING = kRing;
     Tile R[RING];
     const uint32_t c_first = group * cpw;
-    const uint32_t limit = a.limit;
+    // Start-up in three memory rounds (the compiler otherwise loads kernel
+    // arguments lazily, after the limit test, and waits for the staged page
+    // ids with everything else: about six dependent rounds before the first
+    // K/V request). Round 1: kernel arguments (the caller has them). Round 2,
+    // all issued together: the limit, the page id of this wave's first tile
+    // (its position does not depend on the limit), the page ids of the
+    // range, q and the phase0 inputs. Round 3: the first K/V tile. The empty
+    // asm statements with a memory clobber keep each round's requests ahead
+    // of everything after them.
+    const uint32_t t0_first = c_first * C + wave * kTile;
+    uint32_t page_first_raw = 0u;  // clamped only after round 2 (no early wait)
+    if constexpr (PAGE16 && TPW > 0u)
+        page_first_raw = ((const __attribute__((address_space(4))) uint32_t*)(pt))
+            [__builtin_amdgcn_readfirstlane(min(t0_first >> ly.log2p, page_max))];
+    const uint32_t limit_raw =
+        LSRC ? *(const __attribute__((address_space(4))) uint32_t*)(a.limit_src) : a.limit;
+    // Page ids of the block's position range, staged once into LDS (read by
+    // all tiles with a short LDS latency instead of a scalar-cache miss in
+    // front of every tile's loads). Loaded for the range's full extent (cpw
+    // chunks, indices clamped to the table) before the limit is known; only
+    // entries below the range's last position are used.
+    const uint32_t page0 = (c_first * C) >> ly.log2p;
+    const uint32_t npages_full = ((c_first * C + cpw * C - 1u) >> ly.log2p) - page0 + 1u;
+    uint32_t staged_raw = 0u;  // clamped at its LDS store
+    if constexpr (PAGE16)
+        staged_raw = gptr(pt)[min(page0 + min(tid, npages_full - 1u), page_max)];
+    const bool real = tok < kGroup;
+    // q: without phase0 each lane loads its Q^T operand directly; with phase0
+    // thread tid loads dims p and p + 64 (p = tid % 64) of heads 2w, 2w + 1
+    // (w = tid / 64) of this KV head, rotates them with pair p and stages the
+    // rotated rows in LDS (4 rotations per thread instead of 32 per lane).
+    uint4 qr[4];
+    uint16_t qx[2][2];  // phase0: [head 2w + hh][dim p, p + 64]
+    if constexpr (!PH0) {
+        const uint16_t* qsrc = q_row + (kvh * kGroup + (real ? tok : 0u)) * kD + 8u * grp;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) qr[m] = *reinterpret_cast<const uint4*>(qsrc + 32u * m);
+    } else {
+        const uint16_t* qh0 = q_row + (kvh * kGroup + 2u * wave) * kD + (tid & 63u);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            qx[hh][0] = qh0[hh * kD];
+            qx[hh][1] = qh0[hh * kD + 64u];
+        }
+    }
+    const uint32_t t64 = tid & 63u;
+    float invf = 0.f;
+    uint16_t kx = 0, kx2 = 0;
+    uint32_t fresh_v = 0u;
+    if (PH0) {  // every block reads the new token's k/v (a few cached bytes)
+        invf = inv_freq[t64];
+        const uint16_t* kr = q_row + kKCol + kvh * kD;
+        kx = kr[t64];
+        kx2 = kr[t64 + 64u];
+        fresh_v = *reinterpret_cast<const uint32_t*>(q_row + kVCol + kvh * kD + 2u * t64);
+    }
+    // the limit and the first page id arrive together (one wait, at the
+    // limit test below)
+    asm volatile("" ::"s"(limit_raw), "s"(page_first_raw) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t page_first = min(page_first_raw, page_max);
+
+    const uint32_t limit = min(limit_raw, a.pos_max);
     const uint32_t nvalid = min(limit / C + 1u, NC);
     if (c_first >= nvalid) return;  // uniform over the block
     const uint32_t c_end = min(c_first + cpw, nvalid);
@@ -310,12 +379,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         const uint32_t cs = c * C;
         return (limit == 0u || last_pos < cs) ? 0u : (chunk_end(c) - cs) / kTile + 1u;
     };
-    // Page ids of the block's position range, staged once into LDS (read by
-    // all tiles with a short LDS latency instead of a scalar-cache miss in
-    // front of every tile's loads).
-    const uint32_t page0 = (c_first * C) >> ly.log2p;
-    const uint32_t npages_rng = ((min(c_end * C, limit + 1u) - 1u) >> ly.log2p) - page0 + 1u;
-    const bool cached_pages = PAGE16 && npages_rng <= kPageCache;
+    const bool cached_pages = PAGE16 && npages_full <= kPageCache;
     // `from_table` reads the page id from the table itself (scalar path for
     // PAGE16) instead of the LDS copy; the first tiles use it so that they
     // do not wait for the staging barrier.
@@ -325,6 +389,8 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         if constexpr (PAGE16)
             page_u = (cached_pages && !from_table)
                          ? s_pages[__builtin_amdgcn_readfirstlane((t0 >> ly.log2p) - page0)]
+                     : (TPW > 0u && (t0 >> ly.log2p) == (t0_first >> ly.log2p))
+                         ? page_first
                          : table_page(t0);
         load_rows(T, t0, chunk_end(c), page_u);
     };
@@ -400,60 +466,12 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         load_tile(T, cl, j, from_table);
     };
 
-    // Start-up, ordered for latency: (a) loads that need nothing computed
-    // (q, inv_freq, the new token's k/v), (b) the block's page ids, (c) the
-    // first K/V tiles (one dependent scalar load after `limit`), and only
-    // then (d) the work that waits for (a) and (b). Phase0: cos/sin of
-    // position `limit`; the block owning `limit` builds the rotated K and the
-    // V of that token in LDS and stores both to the pool.
+    // Phase0: cos/sin of position `limit`; the block owning `limit` builds
+    // the rotated K and the V of that token in LDS and stores both to the
+    // pool. Without phase0 the owner reads K|V of `limit` from the pool.
     const bool owner = limit / C < c_end && limit < NC * C;
-    const bool real = tok < kGroup;
-    // All start-up loads are unconditional (addresses clamped) so that no
-    // divergent branch makes the compiler wait for them before the first
-    // K/V tiles are issued.
-    // q: without phase0 each lane loads its Q^T operand directly; with phase0
-    // thread tid loads dims p and p + 64 (p = tid % 64) of heads 2w, 2w + 1
-    // (w = tid / 64) of this KV head, rotates them with pair p and stages the
-    // rotated rows in LDS (4 rotations per thread instead of 32 per lane).
-    uint4 qr[4];
-    uint16_t qx[2][2];  // phase0: [head 2w + hh][dim p, p + 64]
-    if constexpr (!PH0) {
-        const uint16_t* qsrc = q_row + (kvh * kGroup + (real ? tok : 0u)) * kD + 8u * grp;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) qr[m] = *reinterpret_cast<const uint4*>(qsrc + 32u * m);
-    } else {
-        const uint16_t* qh0 = q_row + (kvh * kGroup + 2u * wave) * kD + (tid & 63u);
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            qx[hh][0] = qh0[hh * kD];
-            qx[hh][1] = qh0[hh * kD + 64u];
-        }
-    }
-    const uint32_t t64 = tid & 63u;
-    float invf = 0.f;
-    uint16_t kx = 0, kx2 = 0;
-    uint32_t fresh_v = 0u;
     uint2 fresh_kv = make_uint2(0u, 0u);
-    const uint32_t limit_page =
-        owner ? min(((const __attribute__((address_space(4))) uint32_t*)(pt))[limit >> ly.log2p],
-                    page_max)
-              : 0u;
-    if (PH0) {  // every block reads the new token's k/v (a few cached bytes)
-        invf = inv_freq[t64];
-        const uint16_t* kr = q_row + kKCol + kvh * kD;
-        kx = kr[t64];
-        kx2 = kr[t64 + 64u];
-        fresh_v = *reinterpret_cast<const uint32_t*>(q_row + kVCol + kvh * kD + 2u * t64);
-    } else if (owner) {  // K|V of `limit` from the pool, 32 lanes per half
-        const uint16_t* src =
-            pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
-        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-        fresh_kv = __builtin_bit_cast(uint2, *reinterpret_cast<const MCKV_GLOBAL u32x2_t*>(
-                                                 gptr(src + 256u * (t64 >> 5) + (t64 & 31u) * 4u)));
-    }
-    uint32_t staged_page = 0u;
-    if (cached_pages) staged_page = min(gptr(pt)[page0 + min(tid, npages_rng - 1u)], page_max);
-
+    uint32_t limit_page = 0u;
     Tile& A = R[0];
     Tile& B = R[RING > 1u ? 1u : 0u];
     uint32_t ac = c_first, aj = wave;
@@ -466,8 +484,21 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         a_ok = wave < chunk_tiles(c_first) || advance(ac, aj);
         if (a_ok) load_tile(A, ac, aj, true);
     }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (owner)
+        limit_page =
+            min(((const __attribute__((address_space(4))) uint32_t*)(pt))[limit >> ly.log2p],
+                page_max);
+    if (!PH0 && owner) {  // K|V of `limit` from the pool, 32 lanes per half
+        const uint16_t* src =
+            pool + token_base(ly, layer, limit_page, limit & ly.pmask) + kvh * kD;
+        typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+        fresh_kv = __builtin_bit_cast(uint2, *reinterpret_cast<const MCKV_GLOBAL u32x2_t*>(
+                                                 gptr(src + 256u * (t64 >> 5) + (t64 & 31u) * 4u)));
+    }
 
-    if (cached_pages && tid < npages_rng) s_pages[tid] = staged_page;
+    if (cached_pages && tid < npages_full) s_pages[tid] = min(staged_raw, page_max);
     if (PH0) {
         // cos/sin of pair p = tid % 64 (every wave evaluates the same 64)
         float c, sn;
@@ -778,20 +809,31 @@ __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
 template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P, bool FIXED>
 __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
     __attribute__((amdgpu_waves_per_eu(2))) decode_chunk_kernel(
-    const uint16_t* __restrict__ q_rows, const uint32_t* d_pos,
+    const uint16_t* q_rows, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t layer,
     const uint32_t* pt, const uint32_t* const* __restrict__ slot_pt,
     uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
     float* __restrict__ partials, uint32_t NC, uint32_t rec_stride, uint16_t* __restrict__ out,
-    const float* __restrict__ inv_freq, uint32_t C, uint32_t cpw, uint32_t B, bool split,
+    const float* inv_freq, uint32_t C, uint32_t cpw, uint32_t B, bool split,
     unsigned long long* stamps) {
-    const WgStamp stamp(stamps, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
-                        4u, kTlChunkWgs);
+    // Every pointer argument is requested at entry, in one round (the compiler
+    // otherwise loads some of them only where first used, one dependent
+    // round each on the way to the first K/V request).
+    asm volatile("" ::"s"(q_rows), "s"(d_pos), "s"(slot_pos), "s"(pt), "s"(slot_pt), "s"(pool),
+                 "s"(slot_kv), "s"(inv_freq), "s"(layer), "s"(ly.max_pages), "s"(ly.log2p),
+                 "s"(ly.pmask), "s"(C), "s"(cpw), "s"(NC), "s"(stamps));
+    // (the grid size is read only when stamping: it is another argument load)
+    const WgStamp stamp(
+        stamps,
+        stamps != nullptr ? blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z) : 0u,
+        4u, kTlChunkWgs);
     // Positions beyond the pool's capacity do not exist: a limit past it is
     // clamped, so page-table reads stay within its max_pages entries.
     const uint32_t pos_max = pool_pos_max(ly);
     const uint32_t kvh = KV2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : blockIdx.y;
-    auto run = [&](uint32_t slot, uint32_t group, uint32_t limit) {
+    // lsrc: std::true_type when the body reads the limit from limit_src
+    auto run = [&](auto lsrc, uint32_t slot, uint32_t group, uint32_t limit,
+                   const uint32_t* limit_src) {
         DecodeArgs a;
         a.q_row = q_rows + (size_t)slot * kRow;
         a.limit = limit;
@@ -802,8 +844,10 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
         a.split = split;
         a.out = out + (size_t)slot * kHq * kD;
         a.first_data = stamp.p != nullptr ? stamp.p + 3 : nullptr;
-        decode_range_body<PH0, PAGE16, TPW, KV2, FP32P>(a, layer, ly, NC, inv_freq, C, kvh,
-                                                        group, cpw);
+        a.limit_src = limit_src;
+        a.pos_max = pos_max;
+        decode_range_body<PH0, PAGE16, TPW, KV2, FP32P, decltype(lsrc)::value>(
+            a, layer, ly, NC, inv_freq, C, kvh, group, cpw);
     };
     if constexpr (BATCH) {
         if constexpr (FIXED) {
@@ -813,7 +857,7 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
             // round and the scan fewer before its first K/V; measured C3
             // 12.3 against 12.8 us/layer). Slot is the fastest index so the
             // early ranges of all slots are dispatched first.
-            run(blockIdx.x, blockIdx.z, min(*slot_pos[blockIdx.x], pos_max));
+            run(std::true_type{}, blockIdx.x, blockIdx.z, 0u, slot_pos[blockIdx.x]);
             return;
         }
         // Work compaction: the (x, slot) workgroups are numbered densely over
@@ -852,9 +896,10 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
         if (slot >= B) return;  // past the last existing chunk group (uniform)
         const uint32_t end = (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)slot);
         const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)cnt, (int)slot);
-        run(slot, n - (end - c), (uint32_t)__builtin_amdgcn_readlane((int)lim, (int)slot));
+        run(std::false_type{}, slot, n - (end - c),
+            (uint32_t)__builtin_amdgcn_readlane((int)lim, (int)slot), nullptr);
     } else {
-        run(0u, blockIdx.x, min(*d_pos, pos_max));
+        run(std::true_type{}, 0u, blockIdx.x, 0u, d_pos);
     }
 }
 
