@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(128) merge_b_kernel(
     const float* __restrict__ partials2, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
     uint16_t* __restrict__ out, unsigned long long* stamps) {
-    const WgStamp stamp(stamps, blockIdx.x, 2u, kTlMergeWgs);
+    const WgStamp stamp(stamps, 2u, kTlMergeWgs, false);
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
     Loaded<kSplit2> x;
     const float* base = partials2 + ((size_t)slot * kHq + qh) * kSplit2 * kPartial;
@@ -196,7 +196,7 @@ __global__ void __launch_bounds__(128) merge_p_kernel(
     const float* __restrict__ partials, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NC, uint32_t C,
     uint16_t* __restrict__ out, unsigned long long* stamps) {
-    const WgStamp stamp(stamps, blockIdx.x, 2u, kTlMergeWgs);
+    const WgStamp stamp(stamps, 2u, kTlMergeWgs, false);
     const uint32_t slot = blockIdx.x >> 4, qh = blockIdx.x & 15u;
     const float* base = partials + ((size_t)slot * kHq + qh) * NC * kPartial;
     float M, L, A;
@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(256) merge_r_kernel(
     const float* __restrict__ rec, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NR, uint32_t C_rng,
     uint32_t pos_max, uint16_t* __restrict__ out, unsigned long long* stamps) {
-    const WgStamp stamp(stamps, blockIdx.x + gridDim.x * blockIdx.y, 2u, kTlMergeWgs);
+    const WgStamp stamp(stamps, 2u, kTlMergeWgs, false);
     static_assert(Q == 1u || Q == 2u || Q == 4u || Q == 8u, "dim quads per block");
     constexpr uint32_t kSlices = 32u / Q;  // blocks per head
     constexpr uint32_t kLanes = 256u / Q;

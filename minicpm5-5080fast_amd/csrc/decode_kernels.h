@@ -167,6 +167,38 @@ __device__ __forceinline__ uint32_t vdim(uint32_t m, uint32_t h, uint32_t g) {
     return 32u * m + 8u * g + 4u * (h ^ (g & 1u));
 }
 
+// The entry clock is read at once and stored at exit, together with the
+// workgroup's index (computed only then: it needs the grid size, one more
+// argument load), so that nothing of the stamp buffer is waited for at entry.
+struct WgStamp {
+    unsigned long long* stamps;
+    uint32_t words, cap;
+    bool grid3;  // index over a 3-D grid (else blockIdx.x + gridDim.x * blockIdx.y)
+    unsigned long long t_entry;
+    uint32_t xcc;
+    __device__ __forceinline__ WgStamp(unsigned long long* stamps_, uint32_t words_,
+                                       uint32_t cap_, bool grid3_)
+        : stamps(stamps_), words(words_), cap(cap_), grid3(grid3_),
+          t_entry(__builtin_amdgcn_s_memrealtime()),
+          xcc((uint32_t)__builtin_amdgcn_s_getreg(6164)) {}
+    __device__ __forceinline__ unsigned long long* slot() const {
+        if (stamps == nullptr) return nullptr;
+        const uint32_t wg = grid3 ? blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)
+                                  : blockIdx.x + gridDim.x * blockIdx.y;
+        return wg < cap ? stamps + (size_t)words * wg : nullptr;
+    }
+    __device__ __forceinline__ ~WgStamp() {
+        unsigned long long* p = slot();
+        if (p == nullptr) return;
+        if (threadIdx.x == 0u) {
+            p[0] = t_entry;
+            if (words > 2u) p[2] = (unsigned long long)xcc;
+        }
+        if ((threadIdx.x & 63u) == 0u)
+            atomicMax(p + 1, (unsigned long long)__builtin_amdgcn_s_memrealtime());
+    }
+};
+
 struct DecodeArgs {
     const uint16_t* q_row;  // [2560] of this slot
     uint32_t limit;
@@ -177,7 +209,7 @@ struct DecodeArgs {
     bool split;       // record layout per head: false {m, l, acc[128]} rows,
                       // true acc[rec_stride][128] then {m, l}[rec_stride]
     uint16_t* out;    // this slot: [2048]
-    unsigned long long* first_data;  // timeline word for the first tile's arrival, or nullptr
+    const struct WgStamp* stamp;  // debug timeline (the first tile's arrival goes to word 3)
     const uint32_t* limit_src;  // the limit's device word, read by the body when the
                                 // body's LSRC is set (else `limit` holds the limit)
     uint32_t pos_max;           // limits are clamped to this (the pool's last position)
@@ -356,9 +388,10 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
         kx2 = kr[t64 + 64u];
         fresh_v = *reinterpret_cast<const uint32_t*>(q_row + kVCol + kvh * kD + 2u * t64);
     }
-    // the limit and the first page id arrive together (one wait, at the
-    // limit test below)
-    asm volatile("" ::"s"(limit_raw), "s"(page_first_raw) : "memory");
+    // the limit, the first page id and the remaining arguments the K/V
+    // addresses need arrive together (one wait, at the limit test below)
+    asm volatile("" ::"s"(limit_raw), "s"(page_first_raw), "s"(pool), "s"(ly.pmask), "s"(layer)
+                 : "memory");
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t page_first = min(page_first_raw, page_max);
 
@@ -642,14 +675,15 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
                     if (c + ga / TPW < c_end)
                         clamp_load(R[ga % RING], c + ga / TPW, ga % TPW, false);
                     const uint32_t j = wave + 4u * i;
-                    if (h == 0u && i == 0u && a.first_data != nullptr && c == c_first &&
+                    if (h == 0u && i == 0u && a.stamp->stamps != nullptr && c == c_first &&
                         threadIdx.x < 64u) {
                         // timeline: clock at which the first tile's K/V are in
                         // registers (the wait the accumulate below needs anyway)
                         uint32_t k0 = R[0].k[0].x;
                         asm volatile("" : "+v"(k0));
                         if (threadIdx.x == 0u)
-                            *a.first_data = __builtin_amdgcn_s_memrealtime() + (k0 & 0u);
+                            if (unsigned long long* p = a.stamp->slot())
+                                p[3] = __builtin_amdgcn_s_memrealtime() + (k0 & 0u);
                     }
                     if (cc2 < c_end && j < chunk_tiles(cc2))
                         accumulate(xpose(R[g % RING]), cc2 * C + j * kTile, chunk_end(cc2));
@@ -764,22 +798,6 @@ constexpr uint32_t kTlChunkWgs = 8192;
 constexpr uint32_t kTlMergeWgs = 2048;
 constexpr uint32_t kTlWordsPerLaunch = 4u * kTlChunkWgs + 2u * kTlMergeWgs;
 
-struct WgStamp {
-    unsigned long long* p;
-    __device__ __forceinline__ WgStamp(unsigned long long* stamps, uint32_t wg,
-                                       uint32_t words, uint32_t cap)
-        : p(stamps != nullptr && wg < cap ? stamps + (size_t)words * wg : nullptr) {
-        if (p != nullptr && threadIdx.x == 0u) {
-            p[0] = __builtin_amdgcn_s_memrealtime();
-            if (words > 2u) p[2] = (unsigned long long)__builtin_amdgcn_s_getreg(6164);
-        }
-    }
-    __device__ __forceinline__ ~WgStamp() {
-        if (p != nullptr && (threadIdx.x & 63u) == 0u)
-            atomicMax(p + 1, (unsigned long long)__builtin_amdgcn_s_memrealtime());
-    }
-};
-
 // Merge region of a launch's timeline stamps (after the chunk region).
 inline unsigned long long* merge_stamps(unsigned long long* chunk_stamps) {
     return chunk_stamps != nullptr ? chunk_stamps + 4u * kTlChunkWgs : nullptr;
@@ -809,24 +827,27 @@ __device__ __forceinline__ uint32_t n_valid_chunks(uint32_t limit, uint32_t C,
 template <bool PH0, bool BATCH, bool PAGE16, uint32_t TPW, bool KV2, bool FP32P, bool FIXED>
 __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
     __attribute__((amdgpu_waves_per_eu(2))) decode_chunk_kernel(
-    const uint16_t* q_rows, const uint32_t* d_pos,
-    const uint32_t* const* __restrict__ slot_pos, uint32_t layer,
-    const uint32_t* pt, const uint32_t* const* __restrict__ slot_pt,
-    uint16_t* pool, uint16_t* const* __restrict__ slot_kv, DevLayout ly,
-    float* __restrict__ partials, uint32_t NC, uint32_t rec_stride, uint16_t* __restrict__ out,
-    const float* inv_freq, uint32_t C, uint32_t cpw, uint32_t B, bool split,
-    unsigned long long* stamps) {
-    // Every pointer argument is requested at entry, in one round (the compiler
-    // otherwise loads some of them only where first used, one dependent
-    // round each on the way to the first K/V request).
-    asm volatile("" ::"s"(q_rows), "s"(d_pos), "s"(slot_pos), "s"(pt), "s"(slot_pt), "s"(pool),
-                 "s"(slot_kv), "s"(inv_freq), "s"(layer), "s"(ly.max_pages), "s"(ly.log2p),
-                 "s"(ly.pmask), "s"(C), "s"(cpw), "s"(NC), "s"(stamps));
-    // (the grid size is read only when stamping: it is another argument load)
-    const WgStamp stamp(
-        stamps,
-        stamps != nullptr ? blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z) : 0u,
-        4u, kTlChunkWgs);
+    // The first 14 dwords (d_pos .. layer) are what a single-session
+    // workgroup needs before its first K/V request; the decode translation
+    // units are built with kernel-argument preloading, so these arrive in
+    // SGPRs with the wave instead of through a scalar load round (the rest is
+    // requested at entry and needed only later).
+    const uint32_t* d_pos, const uint32_t* pt, const uint16_t* q_rows, const float* inv_freq,
+    uint32_t ly_max_pages, uint32_t ly_log2p, uint32_t C, uint32_t cpw, uint32_t NC,
+    uint32_t layer, uint16_t* pool, uint32_t ly_pmask, uint32_t ly_layers,
+    const uint32_t* const* __restrict__ slot_pos, const uint32_t* const* __restrict__ slot_pt,
+    uint16_t* const* __restrict__ slot_kv, float* __restrict__ partials, uint32_t rec_stride,
+    uint16_t* __restrict__ out, uint32_t B, bool split, unsigned long long* stamps) {
+    // Batched launches: every pointer argument is requested at entry, in one
+    // round (the compiler otherwise loads some of them only where first used,
+    // one dependent round each on the way to the first K/V request). Single
+    // sessions find theirs preloaded.
+    if constexpr (BATCH)
+        asm volatile("" ::"s"(q_rows), "s"(slot_pos), "s"(slot_pt), "s"(slot_kv), "s"(inv_freq),
+                     "s"(layer), "s"(ly_max_pages), "s"(ly_log2p), "s"(ly_pmask), "s"(C),
+                     "s"(cpw), "s"(NC));
+    const WgStamp stamp(stamps, 4u, kTlChunkWgs, true);
+    const DevLayout ly{ly_max_pages, ly_log2p, ly_pmask, ly_layers};
     // Positions beyond the pool's capacity do not exist: a limit past it is
     // clamped, so page-table reads stay within its max_pages entries.
     const uint32_t pos_max = pool_pos_max(ly);
@@ -843,7 +864,7 @@ __global__ void __launch_bounds__(KV2 ? 2 * kThreads : kThreads)
         a.rec_stride = rec_stride;
         a.split = split;
         a.out = out + (size_t)slot * kHq * kD;
-        a.first_data = stamp.p != nullptr ? stamp.p + 3 : nullptr;
+        a.stamp = &stamp;
         a.limit_src = limit_src;
         a.pos_max = pos_max;
         decode_range_body<PH0, PAGE16, TPW, KV2, FP32P, decltype(lsrc)::value>(
@@ -956,9 +977,10 @@ void launch_one(const ChunkLaunch& L) {
     const dim3 block(KV2 ? kHkv * kThreads : kThreads);
 #define MC_CHUNK_LAUNCH(FX, GRID)                                                            \
     hipLaunchKernelGGL((decode_chunk_kernel<PH0, BATCH, PAGE16, TPW, KV2, FP32P, FX>), GRID,  \
-                       block, 0, L.st, L.q, L.d_pos, L.slot_pos, L.layer, L.pt, L.slot_pt,    \
-                       L.pool, L.slot_kv, L.ly, L.partials, L.NC, L.rec_stride, L.out,        \
-                       L.inv_freq, L.C, L.cpw, L.B, L.split, L.stamps)
+                       block, 0, L.st, L.d_pos, L.pt, L.q, L.inv_freq, L.ly.max_pages,        \
+                       L.ly.log2p, L.C, L.cpw, L.NC, L.layer, L.pool, L.ly.pmask,             \
+                       L.ly.num_layers, L.slot_pos, L.slot_pt, L.slot_kv, L.partials,         \
+                       L.rec_stride, L.out, L.B, L.split, L.stamps)
     if constexpr (BATCH && !KV2) {
         if (fixed_map) {
             MC_CHUNK_LAUNCH(true, dim3(L.B, heads, nx));
