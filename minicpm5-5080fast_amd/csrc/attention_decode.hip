@@ -268,7 +268,7 @@ mc_status_t launch_merge(const float* partials, const uint32_t* d_pos,
 // out = bf16(A / L). grid = (16 * 32 / Q slices, B slots).
 template <bool BATCH, uint32_t Q, uint32_t RPT>
 __global__ void __launch_bounds__(256) merge_r_kernel(
-    const float* __restrict__ rec, const uint32_t* d_pos,
+    const float* rec, const uint32_t* d_pos,
     const uint32_t* const* __restrict__ slot_pos, uint32_t NR, uint32_t C_rng,
     uint32_t pos_max, uint16_t* __restrict__ out, unsigned long long* stamps) {
     const WgStamp stamp(stamps, 2u, kTlMergeWgs, false);
@@ -293,7 +293,12 @@ __global__ void __launch_bounds__(256) merge_r_kernel(
         a01[k] = *reinterpret_cast<const float2*>(hb + (size_t)r * kD + d);  // 8-byte aligned
         a23[k] = *reinterpret_cast<const float2*>(hb + (size_t)r * kD + d + 2);
     }
-    const uint32_t limit = min(BATCH ? *slot_pos[slot] : *d_pos, pos_max);  // as the chunk kernel
+    const uint32_t limit_raw = BATCH ? *slot_pos[slot] : *d_pos;
+    // The record loads above stay ahead of the limit test (rec is not
+    // restrict-qualified, so they are ordinary reads that the compiler may not
+    // sink below this clobber): one memory round for records and limit.
+    asm volatile("" ::: "memory");
+    const uint32_t limit = min(limit_raw, pos_max);  // as the chunk kernel
     const uint32_t nr = n_valid_chunks(limit, C_rng, NR);
     if (nr <= 1u) return;  // the chunk kernel wrote the output directly (uniform)
     float mx = -INFINITY;
