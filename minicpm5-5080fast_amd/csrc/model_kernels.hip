@@ -299,7 +299,22 @@ __device__ __forceinline__ void stage_rows(const uint16_t* x, uint32_t ldx,
 // g, u the two dot products rounded to bf16 first (the projection's output
 // rounding), as a gate_up projection followed by the SwiGLU kernel.
 template <uint32_t M, uint32_t PRO, uint32_t KC, bool SWI, uint32_t WV>
-__global__ void __launch_bounds__(64u * WV) gemv_kernel(const GemvArgs a) {
+__global__ void __launch_bounds__(64u * WV)
+    gemv_kernel(const uint16_t* w, const uint16_t* x, const uint16_t* res_in,
+                const uint16_t* addend, const uint16_t* norm_w, uint32_t N, uint32_t ldx,
+                const GemvArgs args) {
+    // The pointers and sizes needed before the first loads come as leading
+    // scalar arguments, which this file's build preloads into SGPRs at wave
+    // launch (no argument load round before the weight and activation
+    // requests); the rest of the arguments is read from the struct.
+    GemvArgs a = args;
+    a.w = w;
+    a.x = x;
+    a.res_in = res_in;
+    a.addend = addend;
+    a.norm_w = norm_w;
+    a.N = N;
+    a.ldx = ldx;
     constexpr uint32_t K = 512u * KC, NCH = K / 8u, T = 64u * WV;
     static_assert(PRO != kProResnorm || K == 2048u, "the norm prologue covers 2048 dims");
     __shared__ uint4 sx[M * NCH];
@@ -677,7 +692,7 @@ void launch_gemv_t(const GemvArgs& a, hipStream_t st) {
     uint32_t blocks = (a.N + WV - 1u) / WV;
     if (blocks > cap) blocks = cap;
     hipLaunchKernelGGL((gemv_kernel<M, PRO, KC, SWI, WV>), dim3(blocks), dim3(64u * WV), 0, st,
-                       a);
+                       a.w, a.x, a.res_in, a.addend, a.norm_w, a.N, a.ldx, a);
 }
 
 template <uint32_t PRO, uint32_t KC, bool SWI = false>
