@@ -124,7 +124,7 @@ constexpr int kNH = kStep / 32;   // 32-key halves per step (one PV MFMA each)
 // Page-id modes of the K/V gather: per row, one page per 64-key step
 // (P >= 64), one page per 32-key half (P = 32).
 constexpr uint32_t kPageRow = 0, kPageStep = 1, kPageHalf = 2;
-constexpr uint32_t kKPitch = 136;  // sK row pitch (bf16): 128 dims + 8
+constexpr uint32_t kKPitch = 144;  // sK row pitch (bf16): 128 dims + 16 (conflict-free K reads)
 constexpr uint32_t kVPitch = 144;  // sV row pitch (bf16): 128 dims + 16 (conflict-free tr reads)
 // LDS operand reads issued this many MFMA blocks ahead of their use (software
 // pipelining written out in the source; 6-16 measured alike, 2% faster than
