@@ -245,13 +245,19 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
     // keeps both in operand layout.
     constexpr bool ROWS = TPW == 1u;
     constexpr bool VROWS = TPW >= 1u;
-    __shared__ __align__(16) uint16_t s_q_[NH][PH0 ? kGroup * kD : 1];  // rotated q rows
+    // Row pitches of the rotated q rows (144 bf16 = 288 B) and the fold's acc
+    // rows (132 fp32 = 528 B): with these the 16-byte reads of q (one row per
+    // lane of a 16-lane group) and the fold's 16-byte writes and reads hit no
+    // LDS bank twice (measured with an LDS probe on gfx950; the unpadded 256 B
+    // and 512 B rows made every such access a 16- to 28-cycle conflict).
+    constexpr uint32_t kQPitch = 144, kAccPitch = kD + 4u;
+    __shared__ __align__(16) uint16_t s_q_[NH][PH0 ? kGroup * kQPitch : 1];  // rotated q rows
     __shared__ __align__(16) uint16_t s_fresh_[NH][256];  // K | V of `limit`
     __shared__ uint32_t s_pages_[NH][kPageCache];         // page ids of this block's range
     // per wave: K and V tile, 16 x 256 B (row loads only)
     __shared__ uint4 s_x_[NH][VROWS ? kWaves : 1u][VROWS ? 2u * 16u * 16u : 1u];
     __shared__ float s_m_[NH][kWaves][kGroup], s_l_[NH][kWaves][kGroup];
-    __shared__ __align__(16) float s_acc_[NH][kWaves][kGroup][kD];
+    __shared__ __align__(16) float s_acc_[NH][kWaves][kGroup][kAccPitch];
     auto& s_q = s_q_[half];
     auto& s_fresh = s_fresh_[half];
     auto& s_pages = s_pages_[half];
@@ -540,7 +546,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const float x = bf16_to_f32(qx[hh][0]), x2 = bf16_to_f32(qx[hh][1]);
-            uint16_t* qd = &s_q[(2u * wave + hh) * kD + p];
+            uint16_t* qd = &s_q[(2u * wave + hh) * kQPitch + p];
             qd[0] = f32_to_bf16(rope_rotate(x, x2, c, sn, true));
             qd[64] = f32_to_bf16(rope_rotate(x2, x, c, sn, false));
         }
@@ -569,7 +575,7 @@ __device__ __forceinline__ void decode_range_body(const DecodeArgs a, uint32_t l
 #pragma unroll
         for (int m = 0; m < 4; ++m)
             qr[m] = *reinterpret_cast<const uint4*>(
-                &s_q[(real ? tok : 0u) * kD + 32u * m + 8u * grp]);
+                &s_q[(real ? tok : 0u) * kQPitch + 32u * m + 8u * grp]);
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) qb[m] = as_bf16x8(real ? qr[m] : make_uint4(0u, 0u, 0u, 0u));
