@@ -405,11 +405,18 @@ __device__ __forceinline__ void prefill_job(
         // S^T blocks: key block kb (keys 16kb + row), lane col = query column.
         f32x4 sacc[kNKB][G];
         {
-            // K operands read kOperandAhead blocks ahead of the MFMAs using them
+            // K operands read kOperandAhead blocks ahead of the MFMAs using them.
+            // Operand o is dim slice m = o / kNKB of key block kb = o % kNKB:
+            // the MFMAs run slice-major, so consecutive MFMAs feed kNKB * G
+            // different accumulators and a chain's next MFMA comes 8 issues
+            // after its previous one (a dependent 16x16x32 MFMA otherwise
+            // waits for its predecessor's result); every accumulator still
+            // sums its slices in order m = 0..3.
             constexpr int kN = 4 * kNKB, kAhead = kOperandAhead;
             bf16x8 ka[kN];
-            auto kread = [&](int i) {
-                const uint16_t* kp = K + (16u * (i / 4) + col) * kKPitch + 32u * (i % 4) + 8u * grp;
+            auto kread = [&](int o) {
+                const int kb = o % kNKB, m = o / kNKB;
+                const uint16_t* kp = K + (16u * kb + col) * kKPitch + 32u * m + 8u * grp;
                 return as_bf16x8(*reinterpret_cast<const uint4*>(kp));
             };
 #pragma unroll
@@ -417,7 +424,7 @@ __device__ __forceinline__ void prefill_job(
 #pragma unroll
             for (int i = 0; i < kN; ++i) {
                 if (i + kAhead < kN) ka[i + kAhead] = kread(i + kAhead);
-                const int kb = i / 4, m = i % 4;
+                const int kb = i % kNKB, m = i / kNKB;
 #pragma unroll
                 for (int g = 0; g < G; ++g)
                     sacc[kb][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
