@@ -94,6 +94,60 @@ __device__ __forceinline__ float block_sum(float x, float* s4) {
     return ((s4[0] + s4[1]) + s4[2]) + s4[3];
 }
 
+// Sums of V (a power of two, at most 16) per-lane values over the 64 lanes,
+// one value per lane group: value j ends in the 64 / V lanes l with
+// l / (64 / V) == j. The pairings run in one fixed order (lanes l and l ^ 32,
+// l ^ 16, the 16-lane mirror, the 8-lane mirror, l ^ 2, l ^ 1); the first
+// log2(V) of them halve the set of values a lane carries (each side keeps
+// one half and adds the partner's copy of it), the rest finish the sum of
+// the one value left. Every value therefore goes through the same addition
+// tree whatever V is, so a column's result does not depend on how many
+// activation rows the launch has.
+// one pairing stage K of lane_reduce_scatter over the first C values
+template <uint32_t K, uint32_t C, uint32_t V>
+__device__ __forceinline__ void lane_pair_stage(float (&v)[V], uint32_t lane) {
+    constexpr uint32_t H = C > 1u ? C / 2u : 1u;  // values after this stage
+#pragma unroll
+    for (uint32_t i = 0; i < H; ++i) {
+        const float u = v[i], w = C > 1u ? v[i + H] : v[i];
+        if constexpr (K < 2u) {
+            // swap: row-even lanes end with (own u, partner u), row-odd lanes
+            // with (partner w, own w); the sum is even + odd
+            const auto a = K == 0u ? __builtin_amdgcn_permlane32_swap(__float_as_uint(u),
+                                                                     __float_as_uint(w), false,
+                                                                     false)
+                                   : __builtin_amdgcn_permlane16_swap(__float_as_uint(u),
+                                                                     __float_as_uint(w), false,
+                                                                     false);
+            v[i] = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+        } else {
+            constexpr int kCtl = K == 2u ? 0x140 : K == 3u ? 0x141 : K == 4u ? 0x4E : 0xB1;
+            const bool right = ((lane >> (5u - K)) & 1u) != 0u;
+            const float keep = right ? w : u, send = right ? u : w;
+            v[i] = keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), kCtl, 0xF,
+                                                                   0xF, false));
+        }
+    }
+}
+
+template <uint32_t V>
+__device__ __forceinline__ float lane_reduce_scatter(float (&v)[V]) {
+    static_assert(V >= 1u && V <= 16u && (V & (V - 1u)) == 0u, "power of two up to 16");
+    const uint32_t lane = threadIdx.x & 63u;
+    // 0: permlane32 swap, 1: permlane16 swap, 2: row mirror, 3: half-row
+    // mirror, 4: quad xor 2, 5: quad xor 1
+    constexpr uint32_t C1 = V > 1u ? V / 2u : 1u, C2 = C1 > 1u ? C1 / 2u : 1u;
+    constexpr uint32_t C3 = C2 > 1u ? C2 / 2u : 1u, C4 = C3 > 1u ? C3 / 2u : 1u;
+    constexpr uint32_t C5 = C4 > 1u ? C4 / 2u : 1u;
+    lane_pair_stage<0u, V>(v, lane);
+    lane_pair_stage<1u, C1>(v, lane);
+    lane_pair_stage<2u, C2>(v, lane);
+    lane_pair_stage<3u, C3>(v, lane);
+    lane_pair_stage<4u, C4>(v, lane);
+    lane_pair_stage<5u, C5>(v, lane);
+    return v[0];
+}
+
 // ---- embedding gather ----
 // grid = rows, block = 256; 16-byte chunks of the hidden row per thread.
 __global__ void __launch_bounds__(kThreads)
@@ -393,18 +447,34 @@ __global__ void __launch_bounds__(64u * WV)
             }
         }
         if (g == NG - 1u) {  // column complete (wave-uniform)
+            // value j = r * MP + m (zero for m >= M), summed over the lanes
+            // at once: value j ends in lanes l >> (6 - log2 V) == j
+            constexpr uint32_t MP = M <= 1u ? 1u : M <= 2u ? 2u : M <= 4u ? 4u : 8u;
+            constexpr uint32_t V = R * MP;
+            constexpr uint32_t kShift = V == 1u ? 6u : V == 2u ? 5u : V == 4u ? 4u
+                                      : V == 8u ? 3u : 2u;
+            float vals[V];
 #pragma unroll
-            for (uint32_t m = 0; m < M; ++m) {
-                float v = wave_sum(acc[0][m]);
-                if constexpr (SWI) {
-                    const float gt = bf16_to_f32(f32_to_bf16(v));
-                    const float up = bf16_to_f32(f32_to_bf16(wave_sum(acc[1][m])));
-                    v = silu_mul(gt, up);
-                }
-                if (lane == m) a.y[(size_t)m * a.ldy + n] = f32_to_bf16(v);
+            for (uint32_t r = 0; r < R; ++r)
 #pragma unroll
-                for (uint32_t r = 0; r < R; ++r) acc[r][m] = 0.f;
+                for (uint32_t m = 0; m < MP; ++m) vals[r * MP + m] = m < M ? acc[r][m] : 0.f;
+            float v = lane_reduce_scatter<V>(vals);
+            const uint32_t j = kShift == 6u ? 0u : lane >> kShift;
+            if constexpr (SWI) {
+                // gate (r = 0) in lanes < 32, up (r = 1) in the lane 32 above
+                const auto gu = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                                 __float_as_uint(v), false, false);
+                const float gt = bf16_to_f32(f32_to_bf16(__uint_as_float(gu[0])));
+                const float up = bf16_to_f32(f32_to_bf16(__uint_as_float(gu[1])));
+                v = silu_mul(gt, up);
             }
+            const uint32_t m = j % MP;
+            if ((kShift == 6u || (lane & ((1u << kShift) - 1u)) == 0u) && j < MP && m < M)
+                a.y[(size_t)m * a.ldy + n] = f32_to_bf16(v);
+#pragma unroll
+            for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+                for (uint32_t m2 = 0; m2 < M; ++m2) acc[r][m2] = 0.f;
         }
         if (!more) break;
 #pragma unroll
