@@ -24,7 +24,9 @@
 // the row (K / 512 of them; whole 1 KB per wave instruction, non-temporal),
 // multiplies them with the matching LDS chunks of each activation row through
 // v_dot2c_f32_bf16 (two bf16 products accumulated in fp32 per instruction),
-// and the 64 lane sums are combined by a fixed butterfly.
+// and the lane sums of all activation rows (and of the gate and up rows) of a
+// column are combined by one reduce-scatter over the 64 lanes with a fixed
+// pairing order (lane_reduce_scatter).
 #include <hip/hip_runtime.h>
 
 #include "error.h"
