@@ -99,6 +99,44 @@ def test_gemv_resnorm(lib, orc, dev, M, add, N):
     assert ok, st
 
 
+@pytest.mark.parametrize("form", ["plain", "plain6144", "resnorm", "resnorm_swiglu"])
+def test_gemv_rows_independent_of_row_count(lib, orc, dev, form):
+    """Every row of an M-row GEMV (M = 1..8, the batch steps) equals the
+    1-row GEMV of that row bit for bit: the lane sums of all rows (and of the
+    gate and up rows) go through one reduce-scatter whose addition tree does
+    not depend on M. This is what keeps batched decode steps equal to solo
+    decodes."""
+    import torch
+    rng = np.random.default_rng(11)
+    K = 6144 if form == "plain6144" else 2048
+    N = 640  # 16-column multiple but not of the grid: ragged wave coverage
+    rows = 2 * N if form == "resnorm_swiglu" else N
+    w = to_dev(rnd_bf16(orc, rng, (rows, K), K ** -0.5), dev)
+    x = to_dev(rnd_bf16(orc, rng, (8, K), 2.0), dev).view(-1)
+    add = to_dev(rnd_bf16(orc, rng, (8, K), 0.5), dev).view(-1)
+    g = to_dev(orc.f32_to_bf16(1 + 0.1 * rng.standard_normal(K, dtype=np.float32)), dev)
+
+    def run(M, xr, ar):
+        y = torch.zeros(M * N, dtype=torch.int16, device=dev)
+        if form.startswith("plain"):
+            st = lib.mc_model_gemv(P(w), P(xr), K, P(y), N, M, N, K, stream())
+        elif form == "resnorm":
+            st = lib.mc_model_gemv_resnorm(P(w), P(xr), P(ar), P(g), None, K, P(y), N, M, N,
+                                           C.c_float(1e-6), stream())
+        else:
+            st = lib.mc_model_gemv_resnorm_swiglu(P(w), P(xr), P(ar), P(g), None, K, P(y), N, M,
+                                                  N, C.c_float(1e-6), stream())
+        assert st == 0
+        torch.cuda.synchronize()
+        return from_dev(y).reshape(M, N)
+
+    solo = [run(1, x[m * K:], add[m * K:]) for m in range(8)]
+    for M in range(2, 9):
+        got = run(M, x, add)
+        for m in range(M):
+            assert np.array_equal(got[m], solo[m][0]), (form, M, m)
+
+
 @pytest.mark.parametrize("M,K", [(1, 6144), (2, 6144), (3, 2048)])
 def test_gemv_swiglu(lib, orc, dev, M, K):
     import torch
