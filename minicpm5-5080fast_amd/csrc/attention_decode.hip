@@ -285,14 +285,21 @@ __global__ void __launch_bounds__(256) merge_r_kernel(
     // Split layout: the head's acc rows [NR][128], then its {m, l} pairs.
     const float* hb = rec + ((size_t)slot * kHq + head) * NR * kPartial;
     const float* hml = hb + (size_t)NR * kD;
+    // Record group k of this lane: records rl + k * kLanes. Single sessions
+    // request every group before the limit (one memory round; a long context
+    // uses them all). Batched slots are ragged and often far shorter than the
+    // buffer (C5: ~2.4 of 17 MB valid), so they request the first group with
+    // the limit and the others only where the limit says they exist.
+    constexpr uint32_t K0 = BATCH ? 1u : RPT;
     float2 ml[RPT], a01[RPT], a23[RPT];
-#pragma unroll
-    for (uint32_t k = 0; k < RPT; ++k) {
+    auto load_group = [&](uint32_t k) {
         const uint32_t r = min(rl + k * kLanes, NR - 1u);
         ml[k] = *reinterpret_cast<const float2*>(hml + 2u * r);
         a01[k] = *reinterpret_cast<const float2*>(hb + (size_t)r * kD + d);  // 8-byte aligned
         a23[k] = *reinterpret_cast<const float2*>(hb + (size_t)r * kD + d + 2);
-    }
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < K0; ++k) load_group(k);
     const uint32_t limit_raw = BATCH ? *slot_pos[slot] : *d_pos;
     // The record loads above stay ahead of the limit test (rec is not
     // restrict-qualified, so they are ordinary reads that the compiler may not
@@ -301,6 +308,15 @@ __global__ void __launch_bounds__(256) merge_r_kernel(
     const uint32_t limit = min(limit_raw, pos_max);  // as the chunk kernel
     const uint32_t nr = n_valid_chunks(limit, C_rng, NR);
     if (nr <= 1u) return;  // the chunk kernel wrote the output directly (uniform)
+#pragma unroll
+    for (uint32_t k = K0; k < RPT; ++k) {
+        if (k * kLanes < nr) {  // uniform over the block
+            load_group(k);
+        } else {  // no record of this group exists; never read below
+            ml[k] = make_float2(0.f, 0.f);
+            a01[k] = a23[k] = make_float2(0.f, 0.f);
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (uint32_t k = 0; k < RPT; ++k)
