@@ -70,23 +70,27 @@ uint32_t mc_kv_prefill_split_kv(uint32_t tokens);
 /* ---- per-session page allocator (PagedKvAllocator, kv_cache.cpp:8-91) ---- */
 typedef struct mc_kv_allocator mc_kv_allocator_t;
 
-/* PagedKvAllocator::init: d_table is a device u32[max_pages], or NULL for a
- * host-only allocator (same page choices and pages_synced accounting, no
+/* PagedKvAllocator::init (kv_cache.cpp:8-22): d_table is a device
+ * u32[max_pages], or NULL for a host-only allocator (same page choices and pages_synced accounting, no
  * copies; used to plan or test tables without a device). */
 mc_status_t mc_kv_allocator_create(uint32_t* d_table, uint32_t max_pages,
                                    uint32_t tokens_per_page,
                                    mc_kv_allocator_t** out);
+/* Frees the allocator object (the reference's is a session member). */
 void mc_kv_allocator_destroy(mc_kv_allocator_t* a);
-/* PagedKvAllocator::ensure_pages_for: lowest-free-page growth to
+/* PagedKvAllocator::ensure_pages_for (kv_cache.cpp:47-84): lowest-free-page growth to
  * ceil(total_tokens/P) pages; H2D of the table prefix only when it grew;
  * MC_E_OUT_OF_MEMORY when the pool is too small. */
 mc_status_t mc_kv_allocator_ensure_pages_for(mc_kv_allocator_t* a,
                                              uint32_t total_tokens, void* stream);
-/* PagedKvAllocator::release_all: clears ownership, keeps device table. */
+/* PagedKvAllocator::release_all (kv_cache.cpp:85-91): clears ownership,
+ * keeps device table. */
 void mc_kv_allocator_release_all(mc_kv_allocator_t* a);
+/* pages_owned() and the pages_synced_ count (kv_cache.h:84,100). */
 uint32_t mc_kv_allocator_pages_owned(const mc_kv_allocator_t* a);
 uint32_t mc_kv_allocator_pages_synced(const mc_kv_allocator_t* a);
-/* Copies min(n, pages_owned) entries of the host shadow table. */
+/* Copies min(n, pages_owned) entries of the host shadow table (shadow_,
+ * kv_cache.h:102). */
 uint32_t mc_kv_allocator_host_table(const mc_kv_allocator_t* a, uint32_t* out,
                                     uint32_t n);
 
@@ -246,11 +250,13 @@ mc_status_t mc_kv_batch_advance(int32_t* const* d_slot_seq,
  * similar mc_debug_* hooks outside it, session.cpp:631-723) ---- */
 
 /* Session state: host seq_len, owned pages, pool layout and the device
- * addresses of the pool and page table (any pointer may be NULL). */
+ * addresses of the pool and page table (any pointer may be NULL). No
+ * reference counterpart (test access to a session's KV state). */
 mc_status_t mc_debug_session_info(mc_session_t session, uint32_t* seq_len,
                                   uint32_t* pages_owned, mc_kv_layout_t* layout,
                                   void** d_pool, void** d_page_table);
-/* Copies the first n token ids of the device sequence (n <= seq_len). */
+/* Copies the first n token ids of the device sequence (n <= seq_len). No
+ * reference counterpart. */
 mc_status_t mc_debug_session_seq(mc_session_t session, int32_t* out, uint32_t n);
 
 /* Session arena bytes (one device allocation per session, sized at create;
@@ -288,11 +294,35 @@ int mc_debug_session_rope_intact(mc_session_t session);
  * into out_ms[0..n) with n == raw_segments and returns n; 0 = off,
  * -1 = bad arguments, -2 = no complete step recorded yet, -3 = HIP error.
  * Call after the step returned (it synchronizes its stream). */
-int mc_debug_breakdown_raw_segments(mc_session_t session);
-int mc_debug_breakdown_bucket_count(void);
-const char* mc_debug_breakdown_bucket_name(int i);
-int mc_debug_breakdown_bucket_of(int raw);
-int mc_debug_breakdown_collect(mc_session_t session, double* out_ms, int n);
+int mc_debug_breakdown_raw_segments(mc_session_t session);   /* session.cpp:686 */
+int mc_debug_breakdown_bucket_count(void);                    /* session.cpp:692 */
+const char* mc_debug_breakdown_bucket_name(int i);            /* session.cpp:696 */
+int mc_debug_breakdown_bucket_of(int raw);                    /* no counterpart */
+int mc_debug_breakdown_collect(mc_session_t session, double* out_ms, int n); /* :705 */
+
+/* Debug dump step limit (reference debug_dump.cpp:152-157, debug_dump.h:
+ * 1-12): with MC_DEBUG_DUMP_DIR set in the environment (read once, with
+ * MC_DEBUG_DUMP_STEPS = N, default 0) forward number t < N of a session with
+ * weights (its counter restarts at mc_session_create / mc_session_reset; each
+ * prefill chunk and each mc_decode_one is one forward) writes, into that
+ * directory, step{t}.logits.f32 (130560 values), step{t}.final_hidden.f32
+ * (the last row after final_norm, 2048) and step{t}.token (int32, the greedy
+ * prediction); the first chunk of a prefill also writes layer{i}.hidden_in,
+ * .attn_out and .mlp_out.f32 (the last row of the residual at the layer's
+ * input, after the o projection's add and after the down projection's add).
+ * Values are the bf16 tensors widened to fp32. A decode step that dumps runs
+ * eagerly (not from the captured graph). This call changes N at run time
+ * (0 stops further dumps); without MC_DEBUG_DUMP_DIR it has no effect. */
+void mc_debug_dump_set_steps(int steps);
+/* Window seed hook of the reference (debug_dump.cpp:159-199): copies rows x
+ * 2048 bf16 host values into the session's residual rows. The reference's
+ * windowed loading (MC_LOAD_LAYERS_MIN/MAX), whose forward starts from such a
+ * seed, is not supported here, so the next mc_prefill's embedding gather
+ * overwrites the rows, as with a fully loaded model in the reference.
+ * MC_E_UNSUPPORTED without weights (as the reference), MC_E_INVALID_ARGUMENT
+ * for rows outside 1..(the session's prefill chunk rows). */
+mc_status_t mc_debug_seed_residual(mc_session_t session, const void* host_bf16_rows,
+                                   uint32_t rows);
 
 /* Batch-group statistics (reference batch_group.cpp:869-886): steps run,
  * their summed wall time (us) and the current member count. */
@@ -310,14 +340,16 @@ int mc_debug_batch_breakdown_collect(mc_batch_group_t group, double* out_ms, int
  * 0xFFFFFFFF = chosen per launch (default). All compute the same softmax;
  * shapes differ in tile boundaries (key splits) and summation order, within
  * the attention tolerance. The previous value is stored to *previous when
- * that is not NULL. Process-wide; for tests that run every shape. */
+ * that is not NULL. Process-wide; for tests that run every shape. No
+ * reference counterpart. */
 mc_status_t mc_kv_debug_prefill_shape(uint32_t shape, uint32_t* previous);
 
 /* Prefill job packing: with key splits off, two to three 32-row jobs per CU
  * and a prefix of at least T/4, one workgroup per CU runs a fixed 2-3 job
  * packing instead of greedy dispatch (identical results). enable = 0 turns it
  * off (default on). The previous setting is stored to *previous when that is
- * not NULL. Process-wide; for tests that compare both schedules. */
+ * not NULL. Process-wide; for tests that compare both schedules. No
+ * reference counterpart. */
 mc_status_t mc_kv_debug_prefill_packing(uint32_t enable, uint32_t* previous);
 
 /* Prefill status of the current device: *barrier_timeouts receives the
@@ -366,7 +398,8 @@ mc_status_t mc_kv_debug_decode_records_only(uint32_t enable, uint32_t* previous)
 #define MC_KV_TIMELINE_WORDS 36864u
 mc_status_t mc_kv_debug_decode_timeline(uint64_t* d_stamps, uint32_t launches);
 
-/* Library build identity, e.g. "minicpm-kv gfx950". */
+/* Library build identity, e.g. "minicpm-kv gfx950". No reference
+ * counterpart. */
 const char* mc_kv_build_info(void);
 
 #pragma GCC visibility pop

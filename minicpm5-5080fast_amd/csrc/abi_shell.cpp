@@ -213,6 +213,7 @@ struct SessionImpl {
     StepGraph step_graph;
     uint64_t graph_launches = 0;
     bool graph_off = false;  // mc_debug_session_set_graph_enabled(s, 0)
+    uint32_t debug_step = 0;  // forwards since create / reset (debug dump step numbers)
     uint32_t rope_snapshot[64] = {};  // inv_freq words at create
     bool rope_snapshot_valid = false;
     Breakdown bd;
@@ -340,7 +341,7 @@ void release_group(GroupImpl* g) {
 
 // Runs the synthetic forward of one prefill chunk: per layer synthetic rows,
 // RoPE + K/V append, paged prefill attention.
-mc_status_t prefill_chunk(SessionImpl& s, uint32_t base, uint32_t n) {
+mc_status_t prefill_chunk(SessionImpl& s, uint32_t base, uint32_t n, bool first) {
     hipStream_t st = s.stream;
     s.h_state.seq_len = base;
     HIP_OR_RETURN(hipMemcpyAsync(&s.d_state->seq_len, &s.h_state.seq_len, sizeof(uint32_t),
@@ -349,7 +350,12 @@ mc_status_t prefill_chunk(SessionImpl& s, uint32_t base, uint32_t n) {
     if (s.model->weights) {
         // the greedy prediction after the chunk's last token goes to
         // d_state.next_token, the token the first decode returns
-        MC_OR_RETURN(forward_prefill(s.fwd, s.d_seq + base, n, &s.d_state->next_token));
+        s.fwd.dump_step = s.debug_step;
+        s.fwd.dump_layers = first;  // layer rows: the first chunk of the prefill
+        const mc_status_t fs =
+            forward_prefill(s.fwd, s.d_seq + base, n, &s.d_state->next_token);
+        s.debug_step += 1;
+        MC_OR_RETURN(fs);
         HIP_OR_RETURN(hipStreamSynchronize(st), "mc_prefill: stream sync failed");
         return prefill_barrier_check("mc_prefill");
     }
@@ -649,6 +655,7 @@ mc_status_t mc_session_reset(mc_session_t session) {
     MC_OR_RETURN(set_device(s->model->device_id, "mc_session_reset"));
     mc_kv_allocator_release_all(s->kv);
     s->seq_len = 0;
+    s->debug_step = 0;
     s->rng_seeded = false;
     s->since_reset = mc_runtime_stats_t{};
     s->h_state = DevState{};
@@ -702,7 +709,7 @@ mc_status_t mc_prefill(mc_session_t session, const int32_t* token_ids,
     for (uint32_t off = 0; off < token_count;) {
         const uint32_t n =
             token_count - off > s->act_rows ? s->act_rows : token_count - off;
-        MC_OR_RETURN(prefill_chunk(*s, base + off, n));
+        MC_OR_RETURN(prefill_chunk(*s, base + off, n, off == 0u));
         off += n;
     }
     s->seq_len = base + token_count;
@@ -774,8 +781,13 @@ mc_status_t mc_decode_one(mc_session_t session, const mc_generation_config_t* co
     hipStream_t st = s->stream;
     MC_OR_RETURN(mc_kv_allocator_ensure_pages_for(s->kv, s->seq_len + 1u, st));
     TraceRange trace_range("mc_decode_one");
-    const bool graph = s->model->use_graphs && !s->graph_off;
+    // a step that writes debug dump files runs eagerly (the files are written
+    // from the host between its kernels)
+    const bool dumping = s->model->weights && dump_due(s->debug_step);
+    const bool graph = s->model->use_graphs && !s->graph_off && !dumping;
     if (s->model->weights) {
+        s->fwd.dump_step = s->debug_step;
+        s->fwd.dump_layers = false;
         // returns the token the previous forward predicted; the forward on it
         // (position seq_len) predicts the next one into d_state.next_token
         HIP_OR_RETURN(hipMemcpyAsync(s->h_emit, &s->d_state->next_token, 4u,
@@ -792,6 +804,7 @@ mc_status_t mc_decode_one(mc_session_t session, const mc_generation_config_t* co
             return forward_decode(s->fwd, &s->d_state->next_token, &s->d_state->next_token,
                                   mark);
         }));
+        s->debug_step += 1;
         if (graph) s->graph_launches += 1;
         MC_OR_RETURN(mc_kv_decode_advance(s->d_seq, &s->d_state->next_token,
                                           &s->d_state->seq_len, st));
@@ -1279,6 +1292,32 @@ int mc_debug_session_rope_intact(mc_session_t session) {
         return -2;
     }
     return std::memcmp(cur, s->rope_snapshot, sizeof(cur)) == 0 ? 1 : 0;
+}
+
+mc_status_t mc_debug_seed_residual(mc_session_t session, const void* host_bf16_rows,
+                                   uint32_t rows) {
+    MC_GUARD_BEGIN
+    SessionImpl* s = session.impl;
+    if (s == nullptr || host_bf16_rows == nullptr) {
+        set_error("mc_debug_seed_residual: session/rows pointer is NULL");
+        return MC_E_INVALID_ARGUMENT;
+    }
+    if (!s->model->weights) {
+        set_error("mc_debug_seed_residual: requires a session of a model loaded with weights "
+                  "(model.wpk)");
+        return MC_E_UNSUPPORTED;
+    }
+    if (rows == 0u || rows > s->fwd.rows) {
+        set_error("mc_debug_seed_residual: rows=%u out of range (1..%u, the prefill chunk rows)",
+                  rows, s->fwd.rows);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    MC_OR_RETURN(set_device(s->model->device_id, "mc_debug_seed_residual"));
+    HIP_OR_RETURN(hipMemcpy(s->fwd.res_a, host_bf16_rows, (size_t)rows * kHidden * 2u,
+                            hipMemcpyHostToDevice),
+                  "mc_debug_seed_residual: H2D copy failed");
+    return MC_OK;
+    MC_GUARD_END
 }
 
 int mc_debug_breakdown_raw_segments(mc_session_t session) {

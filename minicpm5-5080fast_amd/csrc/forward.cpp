@@ -30,7 +30,9 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
 #include <cstdlib>
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -92,7 +94,106 @@ mc_status_t gemm_bf16(const Forward& f, const uint16_t* x, uint32_t M, const uin
 // fits in it and never allocates on its own.
 constexpr size_t kBlasWorkspace = size_t(32) << 20;
 
+// ---- debug dump ----
+struct DumpConfig {
+    bool on = false;
+    int steps = 0;
+    std::string dir;
+};
+DumpConfig& dump_config() {
+    static DumpConfig c = [] {
+        DumpConfig d;
+        const char* dir = std::getenv("MC_DEBUG_DUMP_DIR");
+        if (dir != nullptr && dir[0] != '\0') {
+            const char* n = std::getenv("MC_DEBUG_DUMP_STEPS");
+            d.on = true;
+            d.dir = dir;
+            d.steps = n != nullptr ? std::atoi(n) : 0;
+            std::fprintf(stderr, "[minicpm-native] debug dump enabled: dir=%s steps=%d\n", dir,
+                         d.steps);
+        }
+        return d;
+    }();
+    return c;
+}
+
+// Writes n bf16 values of device memory as fp32 to <dir>/<name> (synchronous).
+mc_status_t dump_bf16(const std::string& name, const uint16_t* d, size_t n, hipStream_t st) {
+    std::vector<uint16_t> h(n);
+    hipError_t e = hipMemcpyAsync(h.data(), d, n * 2u, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("debug dump %s: copy failed: %s", name.c_str(), hipGetErrorString(e));
+        return MC_E_CUDA;
+    }
+    std::vector<float> f(n);
+    for (size_t i = 0; i < n; ++i) f[i] = bf16_to_f32(h[i]);
+    const std::string path = dump_config().dir + "/" + name;
+    FILE* fp = std::fopen(path.c_str(), "wb");
+    if (fp == nullptr) {
+        set_error("debug dump: cannot open %s", path.c_str());
+        return MC_E_IO;
+    }
+    const size_t w = std::fwrite(f.data(), sizeof(float), n, fp);
+    std::fclose(fp);
+    if (w != n) {
+        set_error("debug dump: short write to %s", path.c_str());
+        return MC_E_IO;
+    }
+    return MC_OK;
+}
+
+mc_status_t dump_token(const std::string& name, const int32_t* d_tok, hipStream_t st) {
+    int32_t t = -1;
+    hipError_t e = hipMemcpyAsync(&t, d_tok, 4u, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_error("debug dump %s: copy failed: %s", name.c_str(), hipGetErrorString(e));
+        return MC_E_CUDA;
+    }
+    const std::string path = dump_config().dir + "/" + name;
+    FILE* fp = std::fopen(path.c_str(), "wb");
+    if (fp == nullptr) {
+        set_error("debug dump: cannot open %s", path.c_str());
+        return MC_E_IO;
+    }
+    const size_t w = std::fwrite(&t, sizeof(t), 1, fp);
+    std::fclose(fp);
+    if (w != 1u) {
+        set_error("debug dump: short write to %s", path.c_str());
+        return MC_E_IO;
+    }
+    return MC_OK;
+}
+
+std::string dump_name(const char* kind, uint32_t i, const char* what) {
+    char b[64];
+    std::snprintf(b, sizeof(b), "%s%u.%s", kind, i, what);
+    return b;
+}
+
+// The residual r = bf16(cur + add) of one row into `tmp` (cur unchanged);
+// `normed` receives a normalized copy that is not used.
+mc_status_t residual_row(const uint16_t* cur, const uint16_t* add, uint16_t* tmp,
+                         const uint16_t* norm_w, uint16_t* normed, hipStream_t st) {
+    if (hipMemcpyAsync(tmp, cur, (size_t)kHidden * 2u, hipMemcpyDeviceToDevice, st) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        set_error("debug dump: residual copy failed");
+        return MC_E_CUDA;
+    }
+    if (add == nullptr) return MC_OK;
+    return mc_model_rmsnorm_rows(tmp, add, norm_w, normed, 1, kHidden, kRmsEps, st);
+}
+
 }  // namespace
+
+bool dump_due(uint32_t step) {
+    const DumpConfig& c = dump_config();
+    return c.on && (int64_t)step < (int64_t)c.steps;
+}
 
 mc_status_t prefill_blas_create(void** out, size_t* ws_bytes) {
     *out = nullptr;
@@ -166,10 +267,15 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
     // 444-456), not through the GEMMs and prefill attention.
     if (n == 1u) return forward_decode(f, d_ids, d_next, Marker{});
     uint16_t* res = f.res_a;
+    const bool step_dump = dump_due(f.dump_step);
+    const bool layer_dump = step_dump && f.dump_layers;
+    const uint16_t* res_last = res + (size_t)(n - 1u) * kHidden;
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, res, kHidden, n, st));
     FWD_OR_RETURN(mc_model_rmsnorm_rows(res, nullptr, w.norm1[0], f.normed, n, kHidden, kRmsEps, st));
     const uint32_t S = mc_kv_prefill_split_kv(n);
     for (uint32_t l = 0; l < kModelLayers; ++l) {
+        if (layer_dump)
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "hidden_in.f32"), res_last, kHidden, st));
         FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.qkv[l], kQkvCols, kHidden, f.qkv));
         FWD_OR_RETURN(mc_kv_rope_append(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout, kTheta,
                                         rope_table_off() ? nullptr : f.inv_freq, st));
@@ -178,17 +284,29 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
         FWD_OR_RETURN(gemm_bf16(f, f.attn, n, w.o[l], kHidden, kHidden, f.o_out));
         FWD_OR_RETURN(
             mc_model_rmsnorm_rows(res, f.o_out, w.norm2[l], f.normed, n, kHidden, kRmsEps, st));
+        if (layer_dump)
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "attn_out.f32"), res_last, kHidden, st));
         FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.gate_up[l], 2u * kInter, kHidden, f.gate_up));
         FWD_OR_RETURN(mc_model_swiglu_rows(f.gate_up, f.mlp, n, kInter, st));
         FWD_OR_RETURN(gemm_bf16(f, f.mlp, n, w.down[l], kHidden, kInter, f.down));
         const uint16_t* next_norm = l + 1u < kModelLayers ? w.norm1[l + 1u] : w.final_norm;
         FWD_OR_RETURN(
             mc_model_rmsnorm_rows(res, f.down, next_norm, f.normed, n, kHidden, kRmsEps, st));
+        if (layer_dump)
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "mlp_out.f32"), res_last, kHidden, st));
     }
     FWD_OR_RETURN(mc_model_gemv(w.lm_head, f.normed + (size_t)(n - 1u) * kHidden, kHidden,
                                 f.logits, kVocabSize, 1, kVocabSize, kHidden, st));
-    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v, f.stage_i,
-                                st);
+    FWD_OR_RETURN(mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v,
+                                       f.stage_i, st));
+    if (step_dump) {
+        FWD_OR_RETURN(dump_bf16(dump_name("step", f.dump_step, "final_hidden.f32"),
+                                f.normed + (size_t)(n - 1u) * kHidden, kHidden, st));
+        FWD_OR_RETURN(dump_bf16(dump_name("step", f.dump_step, "logits.f32"), f.logits,
+                                kVocabSize, st));
+        FWD_OR_RETURN(dump_token(dump_name("step", f.dump_step, "token"), d_next, st));
+    }
+    return MC_OK;
 }
 
 mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_next,
@@ -205,8 +323,17 @@ mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_ne
     // package has one, the lm_head on e4m3 weights (forward.cpp:117-130,
     // 444-456)
     const bool q8 = w.fp8_arena != nullptr;
+    // debug dump (eager steps only): residual rows are formed in f.attn (free
+    // between a layer's o projection and the next attention) and normalized
+    // into f.normed (unused by this path)
+    const bool step_dump = dump_due(f.dump_step);
+    const bool layer_dump = step_dump && f.dump_layers;
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_tok, nullptr, cur, kHidden, 1, st));
     for (uint32_t l = 0; l < kModelLayers; ++l) {
+        if (layer_dump) {
+            FWD_OR_RETURN(residual_row(cur, pending, f.attn, w.norm1[l], f.normed, st));
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "hidden_in.f32"), f.attn, kHidden, st));
+        }
         // qkv = W_qkv . norm1(cur + pending); the sum becomes the residual
         uint16_t* res_out = pending != nullptr ? other : nullptr;
         if (q8)
@@ -246,7 +373,19 @@ mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_ne
                                         kInter, st));
         }
         pending = f.down;
+        if (layer_dump) {  // cur: the residual after the o projection
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "attn_out.f32"), cur, kHidden, st));
+            FWD_OR_RETURN(residual_row(cur, pending, f.attn, w.norm1[0], f.normed, st));
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "mlp_out.f32"), f.attn, kHidden, st));
+        }
         mark();
+    }
+    if (step_dump) {  // final_hidden = final_norm(cur + pending)
+        FWD_OR_RETURN(residual_row(cur, pending, f.attn, w.final_norm, f.normed, st));
+        FWD_OR_RETURN(mc_model_rmsnorm_rows(f.attn, nullptr, w.final_norm, f.normed, 1, kHidden,
+                                            kRmsEps, st));
+        FWD_OR_RETURN(dump_bf16(dump_name("step", f.dump_step, "final_hidden.f32"), f.normed,
+                                kHidden, st));
     }
     if (q8 && w.q_lm_head != nullptr)
         FWD_OR_RETURN(mc_model_gemv_fp8_resnorm(w.q_lm_head, w.s_lm_head, cur, pending,
@@ -256,8 +395,14 @@ mc_status_t forward_decode(const Forward& f, const int32_t* d_tok, int32_t* d_ne
         FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur, pending, w.final_norm, nullptr,
                                             kHidden, f.logits, kVocabSize, 1, kVocabSize,
                                             kRmsEps, st));
-    return mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v, f.stage_i,
-                                st);
+    FWD_OR_RETURN(mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v,
+                                       f.stage_i, st));
+    if (step_dump) {
+        FWD_OR_RETURN(dump_bf16(dump_name("step", f.dump_step, "logits.f32"), f.logits,
+                                kVocabSize, st));
+        FWD_OR_RETURN(dump_token(dump_name("step", f.dump_step, "token"), d_next, st));
+    }
+    return MC_OK;
 }
 
 mc_status_t forward_batch(const Forward& f, const BatchKv& b, const Marker& mark) {
@@ -301,3 +446,8 @@ mc_status_t forward_batch(const Forward& f, const BatchKv& b, const Marker& mark
 }
 
 }  // namespace mckv
+
+extern "C" void mc_debug_dump_set_steps(int steps) {
+    mckv::DumpConfig& c = mckv::dump_config();
+    if (c.on) c.steps = steps;
+}

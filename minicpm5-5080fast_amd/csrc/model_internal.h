@@ -85,7 +85,18 @@ struct Forward {
     float* stage_v = nullptr;    // argmax slice results
     int32_t* stage_i = nullptr;
     uint32_t rows = 0;
+    // debug dump (MC_DEBUG_DUMP_DIR): the session's forward counter for this
+    // forward and whether it may dump per-layer rows (the first prefill chunk)
+    uint32_t dump_step = 0;
+    bool dump_layers = false;
 };
+
+// Debug dump of the reference (debug_dump.h:1-12): with MC_DEBUG_DUMP_DIR set
+// (read once) and MC_DEBUG_DUMP_STEPS = N, forward number t < N of a session
+// writes step{t}.logits.f32 / step{t}.final_hidden.f32 / step{t}.token, and a
+// first prefill chunk also layer{i}.hidden_in / attn_out / mlp_out.f32 (the
+// last row), bf16 values widened to fp32, in the golden fixtures' layout.
+bool dump_due(uint32_t step);
 
 // Device bytes of the activation buffers of a Forward with `rows` rows and
 // `logit_rows` logits rows, and their carving from `base` (256-aligned).

@@ -83,6 +83,8 @@ def _bind():
         "mc_debug_session_set_graph_enabled": (None, [Handle, C.c_int]),
         "mc_debug_session_graph_nodes": (C.c_size_t, [Handle]),
         "mc_debug_session_rope_intact": (C.c_int, [Handle]),
+        "mc_debug_seed_residual": (C.c_int, [Handle, C.c_void_p, C.c_uint32]),
+        "mc_debug_dump_set_steps": (None, [C.c_int]),
         "mc_debug_breakdown_raw_segments": (C.c_int, [Handle]),
         "mc_debug_breakdown_collect": (C.c_int, [Handle, C.POINTER(C.c_double), C.c_int]),
         "mc_debug_batch_group_stats": (C.c_int, [Handle, C.POINTER(C.c_uint64),
@@ -186,6 +188,14 @@ class Session:
         (session.cpp:668-686)."""
         return int(_bind().mc_debug_session_rope_intact(self.h))
 
+    def seed_residual(self, rows_bf16) -> None:
+        """mc_debug_seed_residual: rows x 2048 bf16 (uint16 numpy) into the
+        session's residual rows (debug_dump.cpp:159-199)."""
+        import numpy as np
+        a = np.ascontiguousarray(rows_bf16, dtype=np.uint16)
+        check(_bind().mc_debug_seed_residual(self.h, a.ctypes.data, a.size // 2048),
+              "mc_debug_seed_residual")
+
     def last_logits(self):
         """bf16 logits (as float32 numpy) of the session's last forward (a
         model loaded with weights)."""
@@ -267,3 +277,9 @@ class BatchGroup:
 
 __all__ = ["Model", "Session", "BatchGroup", "model_options", "gen_config", "McError",
            "EOS_STREAM_ID"]
+
+
+def dump_set_steps(steps: int) -> None:
+    """mc_debug_dump_set_steps: the debug dump's step limit (effective only
+    when MC_DEBUG_DUMP_DIR was set when the library first checked it)."""
+    _bind().mc_debug_dump_set_steps(int(steps))

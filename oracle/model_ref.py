@@ -95,6 +95,10 @@ class ModelRef:
         self.seq_len = 0
         self.next_token = None
         self.last_logits = None
+        # when a dict: the last row of the residual at each layer's input and
+        # after its two residual adds, and of the final norm's output, keyed
+        # as the reference's debug dump files (debug_dump.h:5-12)
+        self.capture = None
 
     def forward(self, ids) -> int:
         """Runs len(ids) tokens at positions seq_len.. and returns the greedy
@@ -111,21 +115,30 @@ class ModelRef:
             return project(x, w[name])
         res = w["embedding"][np.asarray(ids)]
         normed = rmsnorm(res, w["layer0.norm1"])
+        cap = self.capture
         for l in range(self.layers):
             p = f"layer{l}."
+            if cap is not None:
+                cap[p + "hidden_in"] = np.asarray(res[-1], np.float32).copy()
             qkv = f32_to_bf16(proj(normed, p + "qkv"))
             qkv = np.ascontiguousarray(qkv.reshape(T, QKV))
             rope_append(qkv, T, base, l, self.pt, self.P, self.maxp, THETA, 1, self.pool)
             att = bf16_to_f32(attn_ref(qkv, T, base, l, self.pool, self.pt, self.P, self.maxp))
             o = proj(att, p + "o")
             res = bf16(res + o)
+            if cap is not None:
+                cap[p + "attn_out"] = np.asarray(res[-1], np.float32).copy()
             normed = rmsnorm(res, w[p + "norm2"])
             gu = proj(normed, p + "gate_up")
             mlp = silu_mul(gu[:, :INTER], gu[:, INTER:])
             d = proj(mlp, p + "down")
             res = bf16(res + d)
+            if cap is not None:
+                cap[p + "mlp_out"] = np.asarray(res[-1], np.float32).copy()
             nxt = w[f"layer{l + 1}.norm1"] if l + 1 < self.layers else w["final_norm"]
             normed = rmsnorm(res, nxt)
+        if cap is not None:
+            cap["final_hidden"] = np.asarray(normed[-1], np.float32).copy()
         logits = proj(normed[-1:], "lm_head")[0]
         self.seq_len += T
         self.last_logits = logits

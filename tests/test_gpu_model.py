@@ -491,6 +491,106 @@ def test_model_prefill_decode_vs_oracle(rt, orc, model_dir):
     m.close()
 
 
+_DUMP_CHILD = r"""
+import importlib, json, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+rt = importlib.import_module("minicpm5-5080fast_amd.runtime")
+m = rt.Model(sys.argv[2], rt.model_options(max_context_tokens=4096, max_sessions=1,
+                                           enable_cuda_graph=1))
+s = rt.Session(m)
+s.prefill(json.loads(sys.argv[4]))
+lg = [s.last_logits()]
+cfg = rt.gen_config(max_new_tokens=16)
+toks = []
+for _ in range(4):
+    toks.append(s.decode_one(cfg))
+    lg.append(s.last_logits())
+np.save(sys.argv[3] + "/child_logits.npy", np.stack(lg))
+print(json.dumps(toks))
+s.close()
+m.close()
+"""
+
+
+def test_model_debug_dump_files(rt, orc, model_dir, tmp_path):
+    """The reference's debug dump (debug_dump.h:1-12; MC_DEBUG_DUMP_DIR and
+    MC_DEBUG_DUMP_STEPS, read once, so a child process runs the session):
+    forwards 0..N-1 (the prefill, then each decode) write step{t}.logits /
+    final_hidden / token, the prefill also layer{i}.hidden_in / attn_out /
+    mlp_out (last row, bf16 widened to fp32). The files equal the session's
+    own logits and tokens, and the layer rows and final rows match the
+    oracle's within the logits tolerance. Decode steps that dump run
+    eagerly under a graph-enabled model."""
+    import json
+    import subprocess
+    import sys
+    from oracle import model_ref as R
+    path, w = model_dir
+    d = tmp_path / "dump"
+    d.mkdir()
+    prompt = [1, 500, 130559, 77, 9, 12345, 3, 3, 42]
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, MC_DEBUG_DUMP_DIR=str(d), MC_DEBUG_DUMP_STEPS="3")
+    r = subprocess.run([sys.executable, "-c", _DUMP_CHILD, root, path, str(d),
+                        json.dumps(prompt)], env=env, capture_output=True, text=True,
+                       timeout=600)
+    assert r.returncode == 0, r.stderr[-3000:]
+    toks = json.loads(r.stdout.strip().splitlines()[-1])
+    lg = np.load(d / "child_logits.npy")
+    rd = lambda name, dt=np.float32: np.fromfile(d / name, dtype=dt)
+    for t in range(3):  # forward 0 = the prefill, 1 and 2 = the first decodes
+        assert np.array_equal(rd(f"step{t}.logits.f32"), lg[t]), t
+        assert int(rd(f"step{t}.token", np.int32)[0]) == toks[t], t
+    assert not (d / "step3.logits.f32").exists() and not (d / "step3.token").exists()
+
+    def close(got, want, what):
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert got.shape == want.shape and rel < 2e-2, (what, rel)
+
+    ref = R.ModelRef(w, 42)
+    ref.capture = {}
+    ref.forward(prompt)
+    for l in range(42):
+        for k in ("hidden_in", "attn_out", "mlp_out"):
+            close(rd(f"layer{l}.{k}.f32"), ref.capture[f"layer{l}.{k}"], (l, k))
+    close(rd("step0.final_hidden.f32"), ref.capture["final_hidden"], "step0")
+    ref.capture = {}
+    ref.next_token = toks[0]  # continue from the GPU's token
+    ref.decode()
+    close(rd("step1.final_hidden.f32"), ref.capture["final_hidden"], "step1")
+
+
+def test_model_seed_residual_hook(rt, model_dir, tmp_path):
+    """mc_debug_seed_residual (debug_dump.cpp:159-199): without weights
+    MC_E_UNSUPPORTED; with weights the row count is checked and a seeded
+    session's next prefill is the same as an unseeded one's (its embedding
+    gather starts the forward)."""
+    empty = tmp_path / "nowpk"
+    empty.mkdir()
+    m0 = rt.Model(str(empty), rt.model_options(max_context_tokens=2048, max_sessions=1))
+    s0 = rt.Session(m0)
+    with pytest.raises(rt.McError) as e:
+        s0.seed_residual(np.zeros((1, 2048), dtype=np.uint16))
+    assert e.value.status == 7  # MC_E_UNSUPPORTED
+    s0.close()
+    m0.close()
+    path, _ = model_dir
+    m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2))
+    a, b = rt.Session(m), rt.Session(m)
+    with pytest.raises(rt.McError):
+        a.seed_residual(np.zeros((0, 2048), dtype=np.uint16))
+    rows = np.full((3, 2048), 0x3F80, dtype=np.uint16)
+    a.seed_residual(rows)
+    prompt = [7, 8, 9, 10]
+    a.prefill(prompt)
+    b.prefill(prompt)
+    assert np.array_equal(a.last_logits(), b.last_logits())
+    a.close()
+    b.close()
+    m.close()
+
+
 def test_model_graph_equals_eager_and_batch_equals_solo(rt, model_dir):
     """Greedy tokens and logits: graph replay == eager, and a batch step of two
     sessions == their solo decodes (bitwise)."""
