@@ -529,7 +529,8 @@ def bench_model(pkg, torch, steps):
     """Whole-model greedy decoding with weights: a full-geometry model.wpk of
     random bf16 weights (even / odd layers share one weight set, embedding
     and lm_head one table; the device holds every section separately, 5.03 GB)
-    loaded through mc_model_load with HIP graphs; solo decode after a
+    loaded through mc_model_load with HIP graphs; 2048- and 8448-token
+    prefills (the latter one full prefill chunk), solo decode after the
     2048-token prompt and 8-session batch steps. Each decode streams every
     layer weight and the lm_head once: 4.50 GB per step."""
     import importlib
@@ -580,6 +581,20 @@ def bench_model(pkg, torch, steps):
         for x in ss + [s]:
             x.close()
         m.close()
+        # one full prefill chunk (8448 rows per projection GEMM), on a model
+        # whose context holds it
+        m = rt.Model(d, rt.model_options(max_context_tokens=16896, max_sessions=1,
+                                         enable_cuda_graph=1))
+        s = rt.Session(m)
+        long_prompt = [(i * 7919) % W.VOCAB for i in range(8448)]
+        s.prefill(long_prompt)
+        s.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        s.prefill(long_prompt)
+        prefill_long_s = time.perf_counter() - t0
+        s.close()
+        m.close()
         # FP8 mode (precision MC_FP8): model_fp8.wpk beside model.wpk, e4m3
         # codes of normal samples (fp32 bits cut to e4m3) with row scales;
         # each decode streams the e4m3 projections and lm_head, 2.25 GB
@@ -618,6 +633,8 @@ def bench_model(pkg, torch, steps):
         "weights": "random bf16, full MiniCPM5-2B geometry (42 layers, vocab 130560)",
         "load_s": load_s, "weight_bytes_per_step": weight_bytes,
         "prefill_2048_ms": prefill_s * 1e3, "prefill_tokens_per_s": 2048 / prefill_s,
+        "prefill_8448_ms": prefill_long_s * 1e3,
+        "prefill_8448_tokens_per_s": 8448 / prefill_long_s,
         "decode_ms_per_token": solo * 1e3, "decode_tokens_per_s": 1.0 / solo,
         "decode_weight_gbs": weight_bytes / solo / 1e9,
         "decode_pct_hbm_peak": 100.0 * weight_bytes / solo / 1e9 / HBM_PEAK_GBS,

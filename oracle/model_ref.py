@@ -104,6 +104,9 @@ class ModelRef:
         """Runs len(ids) tokens at positions seq_len.. and returns the greedy
         prediction after the last one (also kept as next_token)."""
         w, T, base = self.w, len(ids), self.seq_len
+        if base + T > self.maxp * self.P:  # the C helpers write the pool unchecked
+            raise ValueError(f"ModelRef: {base + T} tokens exceed max_ctx "
+                             f"{self.maxp * self.P}")
 
         def proj(x, name):
             if T == 1 and self.fp8 is not None and name in self.fp8:

@@ -561,6 +561,52 @@ def test_model_debug_dump_files(rt, orc, model_dir, tmp_path):
     close(rd("step1.final_hidden.f32"), ref.capture["final_hidden"], "step1")
 
 
+_GEMM_CHILD = r"""
+import importlib, json, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+rt = importlib.import_module("minicpm5-5080fast_amd.runtime")
+m = rt.Model(sys.argv[2], rt.model_options(max_context_tokens=8448, max_sessions=1))
+s = rt.Session(m)
+out = []
+for n in json.loads(sys.argv[4]):
+    s.reset()
+    s.prefill([(i * 7919) % 130560 for i in range(n)])
+    out.append(s.last_logits())
+np.save(sys.argv[3], np.stack(out))
+s.close()
+m.close()
+"""
+
+
+def test_model_tuned_gemm_solutions_match_default(rt, model_dir, tmp_path):
+    """The prefill projections' tuned rocBLAS solutions (prefill_gemm_table.h)
+    against rocBLAS's default heuristic (MC_PREFILL_GEMM_DEFAULT=1, read once,
+    so in a child process): the last-row logits of prefills whose row counts
+    select tuned rows (300 rows: the 256-row gate_up row; 8448 rows, one full
+    chunk: gate_up and down) agree to the logits tolerance. Only the GEMMs'
+    summation order differs."""
+    import json
+    import subprocess
+    import sys
+    path, _ = model_dir
+    sizes = [300, 8448]
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = {}
+    for tag, extra in (("tuned", {}), ("default", {"MC_PREFILL_GEMM_DEFAULT": "1"})):
+        env = {k: v for k, v in os.environ.items() if k != "MC_PREFILL_GEMM_DEFAULT"}
+        env.update(extra)
+        f = str(tmp_path / f"{tag}.npy")
+        r = subprocess.run([sys.executable, "-c", _GEMM_CHILD, root, path, f, json.dumps(sizes)],
+                           env=env, capture_output=True, text=True, timeout=600)
+        assert r.returncode == 0, r.stderr[-3000:]
+        out[tag] = np.load(f)
+    for i, n in enumerate(sizes):
+        rel, cos = compare_logits(out["tuned"][i], out["default"][i])
+        print("rows", n, "rel", rel, "cos", cos)
+        assert rel < 2e-2 and cos > 0.999, n
+
+
 def test_model_seed_residual_hook(rt, model_dir, tmp_path):
     """mc_debug_seed_residual (debug_dump.cpp:159-199): without weights
     MC_E_UNSUPPORTED; with weights the row count is checked and a seeded
