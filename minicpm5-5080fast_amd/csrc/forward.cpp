@@ -26,11 +26,10 @@
 //     workgroups still reading the old one. Attention is the phase0 decode
 //     (RoPE + K/V append + split-KV attention in one chunk kernel).
 #include <hip/hip_runtime.h>
-// rocblas_gemm_ex_get_solutions is declared under the beta feature API.
-#define ROCBLAS_BETA_FEATURES_API
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -84,6 +83,10 @@ const PrefillGemmTable* gemm_table() {
     return t;
 }
 
+static_assert(sizeof(kPrefillGemmRocm) / sizeof(kPrefillGemmRocm[0]) <= 64u &&
+                  sizeof(kPrefillGemmTorch) / sizeof(kPrefillGemmTorch[0]) <= 64u,
+              "a table row is one bit of gemm_bf16's rejection mask");
+
 // Row of the tuned table for an M x N x K projection: the largest tuned M not
 // above M; -1 below the smallest, for other shapes or without a table.
 int gemm_row(const PrefillGemmTable* t, uint32_t M, uint32_t N, uint32_t K) {
@@ -97,11 +100,11 @@ int gemm_row(const PrefillGemmTable* t, uint32_t M, uint32_t N, uint32_t K) {
 }
 
 // y[M][N] = x[M][K] . W[N][K]^T through rocBLAS (column-major view: C(N x M) =
-// W^T(N x K) . x^T(K x M)), with the tuned solution of the shape. The first
-// call of a table row on a handle checks that rocBLAS lists the row's index
-// among the shape's solutions (rocblas_gemm_ex_get_solutions); one it does
-// not list leaves that row on the default heuristic, as does
-// MC_PREFILL_GEMM_DEFAULT=1 for every row (the measured A/B of the tables).
+// W^T(N x K) . x^T(K x M)), with the tuned solution of the shape. An index
+// that rocBLAS rejects (it checks one against the problem before launching)
+// reruns the call on the default heuristic and leaves that table row on it
+// for the rest of the process, as MC_PREFILL_GEMM_DEFAULT=1 does for every
+// row (the measured A/B of the tables).
 mc_status_t gemm_bf16(const Forward& f, const uint16_t* x, uint32_t M, const uint16_t* W,
                       uint32_t N, uint32_t K, uint16_t* y) {
     rocblas_handle h = static_cast<rocblas_handle>(f.blas);
@@ -118,37 +121,20 @@ mc_status_t gemm_bf16(const Forward& f, const uint16_t* x, uint32_t M, const uin
             (rocblas_int)N, y, rocblas_datatype_bf16_r, (rocblas_int)N, rocblas_datatype_f32_r,
             idx ? rocblas_gemm_algo_solution_index : rocblas_gemm_algo_standard, idx, 0);
     };
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Wdeprecated-declarations"
-    auto list = [&](rocblas_int* out, rocblas_int* n) {
-        return rocblas_gemm_ex_get_solutions(
-            h, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)N,
-            (rocblas_int)M, (rocblas_int)K, &alpha, W, rocblas_datatype_bf16_r, (rocblas_int)K, x,
-            rocblas_datatype_bf16_r, (rocblas_int)K, &beta, y, rocblas_datatype_bf16_r,
-            (rocblas_int)N, y, rocblas_datatype_bf16_r, (rocblas_int)N, rocblas_datatype_f32_r,
-            rocblas_gemm_algo_solution_index, 0, out, n);
-    };
-#pragma clang diagnostic pop
     const PrefillGemmTable* t = gemm_table();
     const int row = gemm_row(t, M, N, K);
-    int32_t idx = 0;
-    if (row >= 0 && t->rows[row].index != 0) {
-        const uint64_t bit = uint64_t(1) << row;
-        if (!(f.gemm_checked & bit)) {
-            f.gemm_checked |= bit;
-            rocblas_int n = 0;
-            if (list(nullptr, &n) == rocblas_status_success && n > 0) {
-                std::vector<rocblas_int> ids((size_t)n);
-                if (list(ids.data(), &n) == rocblas_status_success &&
-                    std::find(ids.begin(), ids.begin() + n, t->rows[row].index) !=
-                        ids.begin() + n)
-                    f.gemm_valid |= bit;
-            }
-        }
-        if (f.gemm_valid & bit) idx = t->rows[row].index;
-    }
+    // rows whose index this process's rocBLAS rejected (it validates an index
+    // before launching anything)
+    static std::atomic<uint64_t> rejected{0};
+    const uint64_t bit = row >= 0 ? uint64_t(1) << row : 0u;
+    const int32_t idx = row >= 0 && !(rejected.load(std::memory_order_relaxed) & bit)
+                            ? t->rows[row].index
+                            : 0;
     rocblas_status s = run(idx);
-    if (s != rocblas_status_success && idx != 0) s = run(0);
+    if (s != rocblas_status_success && idx != 0) {
+        rejected.fetch_or(bit, std::memory_order_relaxed);
+        s = run(0);
+    }
     if (s != rocblas_status_success) {
         set_error("prefill GEMM (%u x %u x %u): rocblas_gemm_ex failed: %s", M, N, K,
                   rocblas_status_to_string(s));

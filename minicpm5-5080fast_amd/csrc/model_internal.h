@@ -68,9 +68,6 @@ struct Forward {
     const ModelWeights* w = nullptr;
     hipStream_t st = nullptr;
     void* blas = nullptr;  // rocblas_handle for the prefill GEMMs
-    // Tuned-solution rows of the prefill GEMM table (bit i = row i) already
-    // looked up in rocBLAS's solution list on this handle, and those found.
-    mutable uint64_t gemm_checked = 0, gemm_valid = 0;
     // KV cache of a session (prefill and solo decode)
     uint16_t* pool = nullptr;
     const uint32_t* d_pt = nullptr;
