@@ -9,7 +9,7 @@ the headline workload C4 (one session, 131072 cached tokens in 2048 pages of
 second over the whole timed region (inputs resident in HBM); the other
 configurations are reported under "configs".
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,c5,pf,alloc]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,c5,pf,alloc,model,mprefill]
 """
 from __future__ import annotations
 
@@ -525,6 +525,46 @@ def cpu_baseline(seconds: float):
     }
 
 
+def model_long_prefill(rt, W, torch, d, reps=1):
+    """Seconds of one 8448-token prefill (one full prefill chunk: 8448 rows
+    per projection GEMM) on a model whose context holds it, after one
+    untimed prefill that loads the GEMM kernels; the mean of `reps`."""
+    m = rt.Model(d, rt.model_options(max_context_tokens=16896, max_sessions=1,
+                                     enable_cuda_graph=1))
+    s = rt.Session(m)
+    prompt = [(i * 7919) % W.VOCAB for i in range(8448)]
+    s.prefill(prompt)
+    total = 0.0
+    for _ in range(reps):
+        s.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        s.prefill(prompt)
+        total += time.perf_counter() - t0
+    s.close()
+    m.close()
+    return total / reps
+
+
+def bench_model_prefill(pkg, torch, reps):
+    """Whole-model 8448-token prefill alone (random-weight model.wpk of the
+    full geometry, as in bench_model)."""
+    import importlib
+    import shutil
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    W = importlib.import_module("wpk_util")
+    rt = importlib.import_module("minicpm5-5080fast_amd.runtime")
+    d = tempfile.mkdtemp(prefix="mc_wpk_")
+    try:
+        W.write_wpk(os.path.join(d, "model.wpk"), W.model_sections(2), W.random_blobs(7, 2))
+        sec = model_long_prefill(rt, W, torch, d, reps)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return {"weights": "random bf16, full MiniCPM5-2B geometry (42 layers, vocab 130560)",
+            "reps": reps, "prefill_8448_ms": sec * 1e3, "prefill_8448_tokens_per_s": 8448 / sec}
+
+
 def bench_model(pkg, torch, steps):
     """Whole-model greedy decoding with weights: a full-geometry model.wpk of
     random bf16 weights (even / odd layers share one weight set, embedding
@@ -581,20 +621,7 @@ def bench_model(pkg, torch, steps):
         for x in ss + [s]:
             x.close()
         m.close()
-        # one full prefill chunk (8448 rows per projection GEMM), on a model
-        # whose context holds it
-        m = rt.Model(d, rt.model_options(max_context_tokens=16896, max_sessions=1,
-                                         enable_cuda_graph=1))
-        s = rt.Session(m)
-        long_prompt = [(i * 7919) % W.VOCAB for i in range(8448)]
-        s.prefill(long_prompt)
-        s.reset()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        s.prefill(long_prompt)
-        prefill_long_s = time.perf_counter() - t0
-        s.close()
-        m.close()
+        prefill_long_s = model_long_prefill(rt, W, torch, d)
         # FP8 mode (precision MC_FP8): model_fp8.wpk beside model.wpk, e4m3
         # codes of normal samples (fp32 bits cut to e4m3) with row scales;
         # each decode streams the e4m3 projections and lm_head, 2.25 GB
@@ -730,6 +757,10 @@ def main():
         res["model_decode"] = bench_model(pkg, torch, max(8, args.steps))
         log(res["model_decode"])
         torch.cuda.empty_cache()
+    if "mprefill" in cfgs:
+        log("whole model with weights: 8448-token prefill ...")
+        res["model_prefill"] = bench_model_prefill(pkg, torch, max(1, min(args.steps, 10)))
+        log(res["model_prefill"])
     if "pf" in cfgs:
         for base in (0, 8448):
             log(f"prefill attention 8448 tokens at base {base} ...")
