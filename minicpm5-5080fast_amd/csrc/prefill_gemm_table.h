@@ -33,57 +33,89 @@ struct PrefillGemmTable {
 // /opt/rocm rocBLAS 5.2.0.5b515cf1bc. Ascending m within each (n, k).
 inline constexpr PrefillGemmSolution kPrefillGemmRocm[] = {
     {256, 2560, 2048, 0},  // default 9.6 us, chosen 9.6 us
-    {256, 2048, 2048, 0},  // default 8.9 us, chosen 8.9 us
-    {256, 12288, 2048, 438638},  // default 20.0 us, chosen 15.3 us
-    {256, 2048, 6144, 439289},  // default 50.3 us, chosen 17.8 us
-    {512, 2560, 2048, 438699},  // default 12.8 us, chosen 11.4 us
-    {512, 2048, 2048, 438490},  // default 10.3 us, chosen 9.9 us
-    {512, 12288, 2048, 438908},  // default 25.9 us, chosen 23.8 us
-    {512, 2048, 6144, 438490},  // default 22.1 us, chosen 21.1 us
-    {1024, 2560, 2048, 438498},  // default 16.4 us, chosen 15.2 us
-    {1024, 2048, 2048, 439044},  // default 13.9 us, chosen 12.6 us
-    {1024, 12288, 2048, 0},  // default 39.4 us, chosen 39.4 us
-    {1024, 2048, 6144, 438703},  // default 52.3 us, chosen 31.3 us
-    {2048, 2560, 2048, 438991},  // default 23.0 us, chosen 21.9 us
-    {2048, 2048, 2048, 438649},  // default 23.3 us, chosen 18.3 us
-    {2048, 12288, 2048, 0},  // default 74.7 us, chosen 74.7 us
-    {2048, 2048, 6144, 439119},  // default 56.5 us, chosen 46.5 us
-    {4096, 2560, 2048, 0},  // default 35.8 us, chosen 35.8 us
-    {4096, 2048, 2048, 0},  // default 27.8 us, chosen 27.8 us
-    {4096, 12288, 2048, 0},  // default 129.4 us, chosen 129.4 us
-    {4096, 2048, 6144, 439189},  // default 92.3 us, chosen 71.8 us
-    {8448, 2560, 2048, 438853},  // default 73.0 us, chosen 70.6 us
-    {8448, 2048, 2048, 439422},  // default 65.4 us, chosen 57.0 us
-    {8448, 12288, 2048, 440238},  // default 341.6 us, chosen 282.4 us
-    {8448, 2048, 6144, 439217},  // default 164.6 us, chosen 156.1 us
+    {256, 2048, 2048, 0},  // default 8.8 us, chosen 8.8 us
+    {256, 12288, 2048, 438638},  // default 20.0 us, chosen 15.5 us
+    {256, 2048, 6144, 439289},  // default 50.5 us, chosen 17.9 us
+    {512, 2560, 2048, 438699},  // default 12.7 us, chosen 11.3 us
+    {512, 2048, 2048, 438490},  // default 10.4 us, chosen 9.7 us
+    {512, 12288, 2048, 438908},  // default 26.4 us, chosen 24.1 us
+    {512, 2048, 6144, 438490},  // default 22.2 us, chosen 21.3 us
+    {1024, 2560, 2048, 438829},  // default 16.5 us, chosen 15.3 us
+    {1024, 2048, 2048, 439044},  // default 13.8 us, chosen 12.8 us
+    {1024, 12288, 2048, 0},  // default 40.0 us, chosen 40.0 us
+    {1024, 2048, 6144, 438703},  // default 52.4 us, chosen 32.0 us
+    {2048, 2560, 2048, 438280},  // default 23.6 us, chosen 21.9 us
+    {2048, 2048, 2048, 438785},  // default 23.4 us, chosen 18.4 us
+    {2048, 12288, 2048, 0},  // default 77.4 us, chosen 77.4 us
+    {2048, 2048, 6144, 438785},  // default 56.6 us, chosen 47.6 us
+    {3072, 2560, 2048, 439190},  // default 30.6 us, chosen 27.1 us
+    {3072, 2048, 2048, 438994},  // default 26.6 us, chosen 23.1 us
+    {3072, 12288, 2048, 0},  // default 116.9 us, chosen 116.9 us
+    {3072, 2048, 6144, 438280},  // default 85.3 us, chosen 60.7 us
+    {4096, 2560, 2048, 438853},  // default 36.6 us, chosen 35.0 us
+    {4096, 2048, 2048, 0},  // default 28.5 us, chosen 28.5 us
+    {4096, 12288, 2048, 0},  // default 131.8 us, chosen 131.8 us
+    {4096, 2048, 6144, 439189},  // default 93.5 us, chosen 73.5 us
+    {5120, 2560, 2048, 438973},  // default 45.3 us, chosen 40.2 us
+    {5120, 2048, 2048, 0},  // default 33.3 us, chosen 33.3 us
+    {5120, 12288, 2048, 439306},  // default 191.6 us, chosen 175.4 us
+    {5120, 2048, 6144, 439046},  // default 93.7 us, chosen 86.6 us
+    {6144, 2560, 2048, 0},  // default 44.3 us, chosen 44.3 us
+    {6144, 2048, 2048, 438853},  // default 41.1 us, chosen 38.6 us
+    {6144, 12288, 2048, 440238},  // default 263.7 us, chosen 211.8 us
+    {6144, 2048, 6144, 439306},  // default 107.8 us, chosen 102.2 us
+    {7168, 2560, 2048, 439434},  // default 67.4 us, chosen 57.7 us
+    {7168, 2048, 2048, 0},  // default 43.6 us, chosen 43.6 us
+    {7168, 12288, 2048, 439080},  // default 272.5 us, chosen 252.3 us
+    {7168, 2048, 6144, 439285},  // default 121.8 us, chosen 113.4 us
+    {8448, 2560, 2048, 438853},  // default 75.1 us, chosen 71.5 us
+    {8448, 2048, 2048, 439422},  // default 68.4 us, chosen 58.2 us
+    {8448, 12288, 2048, 440238},  // default 365.5 us, chosen 292.0 us
+    {8448, 2048, 6144, 439253},  // default 168.5 us, chosen 159.2 us
 };
 
 // PyTorch's bundled rocBLAS 5.0.2.20250912-42-1199-g2584e35062.
 inline constexpr PrefillGemmSolution kPrefillGemmTorch[] = {
-    {256, 2560, 2048, 0},  // default 17.0 us, chosen 17.0 us
-    {256, 2048, 2048, 0},  // default 16.0 us, chosen 16.0 us
-    {256, 12288, 2048, 618501},  // default 22.8 us, chosen 20.3 us
-    {256, 2048, 6144, 0},  // default 19.0 us, chosen 19.0 us
+    {256, 2560, 2048, 0},  // default 16.0 us, chosen 16.0 us
+    {256, 2048, 2048, 0},  // default 19.9 us, chosen 19.9 us
+    {256, 12288, 2048, 618509},  // default 22.9 us, chosen 20.7 us
+    {256, 2048, 6144, 0},  // default 18.6 us, chosen 18.6 us
     {512, 2560, 2048, 0},  // default 16.3 us, chosen 16.3 us
-    {512, 2048, 2048, 0},  // default 16.2 us, chosen 16.2 us
-    {512, 12288, 2048, 0},  // default 26.6 us, chosen 26.6 us
-    {512, 2048, 6144, 0},  // default 21.8 us, chosen 21.8 us
-    {1024, 2560, 2048, 0},  // default 19.0 us, chosen 19.0 us
-    {1024, 2048, 2048, 0},  // default 15.3 us, chosen 15.3 us
-    {1024, 12288, 2048, 0},  // default 42.1 us, chosen 42.1 us
-    {1024, 2048, 6144, 0},  // default 35.0 us, chosen 35.0 us
-    {2048, 2560, 2048, 0},  // default 25.7 us, chosen 25.7 us
-    {2048, 2048, 2048, 0},  // default 20.9 us, chosen 20.9 us
-    {2048, 12288, 2048, 0},  // default 81.9 us, chosen 81.9 us
-    {2048, 2048, 6144, 0},  // default 48.6 us, chosen 48.6 us
-    {4096, 2560, 2048, 618612},  // default 40.0 us, chosen 38.0 us
-    {4096, 2048, 2048, 0},  // default 31.2 us, chosen 31.2 us
-    {4096, 12288, 2048, 0},  // default 138.0 us, chosen 138.0 us
-    {4096, 2048, 6144, 0},  // default 77.4 us, chosen 77.4 us
-    {8448, 2560, 2048, 0},  // default 75.4 us, chosen 75.4 us
-    {8448, 2048, 2048, 0},  // default 65.6 us, chosen 65.6 us
-    {8448, 12288, 2048, 618612},  // default 608.6 us, chosen 300.5 us
-    {8448, 2048, 6144, 618468},  // default 352.7 us, chosen 167.3 us
+    {512, 2048, 2048, 0},  // default 17.4 us, chosen 17.4 us
+    {512, 12288, 2048, 0},  // default 26.7 us, chosen 26.7 us
+    {512, 2048, 6144, 0},  // default 22.0 us, chosen 22.0 us
+    {1024, 2560, 2048, 0},  // default 18.9 us, chosen 18.9 us
+    {1024, 2048, 2048, 0},  // default 16.1 us, chosen 16.1 us
+    {1024, 12288, 2048, 0},  // default 42.7 us, chosen 42.7 us
+    {1024, 2048, 6144, 0},  // default 34.9 us, chosen 34.9 us
+    {2048, 2560, 2048, 0},  // default 25.5 us, chosen 25.5 us
+    {2048, 2048, 2048, 0},  // default 20.8 us, chosen 20.8 us
+    {2048, 12288, 2048, 0},  // default 82.7 us, chosen 82.7 us
+    {2048, 2048, 6144, 0},  // default 49.3 us, chosen 49.3 us
+    {3072, 2560, 2048, 0},  // default 30.6 us, chosen 30.6 us
+    {3072, 2048, 2048, 0},  // default 26.2 us, chosen 26.2 us
+    {3072, 12288, 2048, 0},  // default 125.2 us, chosen 125.2 us
+    {3072, 2048, 6144, 0},  // default 65.2 us, chosen 65.2 us
+    {4096, 2560, 2048, 618613},  // default 40.7 us, chosen 38.4 us
+    {4096, 2048, 2048, 0},  // default 31.5 us, chosen 31.5 us
+    {4096, 12288, 2048, 0},  // default 140.6 us, chosen 140.6 us
+    {4096, 2048, 6144, 0},  // default 80.1 us, chosen 80.1 us
+    {5120, 2560, 2048, 0},  // default 42.2 us, chosen 42.2 us
+    {5120, 2048, 2048, 0},  // default 37.4 us, chosen 37.4 us
+    {5120, 12288, 2048, 618614},  // default 193.3 us, chosen 185.7 us
+    {5120, 2048, 6144, 0},  // default 95.5 us, chosen 95.5 us
+    {6144, 2560, 2048, 0},  // default 45.5 us, chosen 45.5 us
+    {6144, 2048, 2048, 0},  // default 42.2 us, chosen 42.2 us
+    {6144, 12288, 2048, 618614},  // default 470.5 us, chosen 227.1 us
+    {6144, 2048, 6144, 0},  // default 109.1 us, chosen 109.1 us
+    {7168, 2560, 2048, 618468},  // default 74.5 us, chosen 70.4 us
+    {7168, 2048, 2048, 0},  // default 43.9 us, chosen 43.9 us
+    {7168, 12288, 2048, 618612},  // default 278.8 us, chosen 258.0 us
+    {7168, 2048, 6144, 0},  // default 116.8 us, chosen 116.8 us
+    {8448, 2560, 2048, 0},  // default 75.0 us, chosen 75.0 us
+    {8448, 2048, 2048, 0},  // default 65.8 us, chosen 65.8 us
+    {8448, 12288, 2048, 618612},  // default 565.3 us, chosen 300.3 us
+    {8448, 2048, 6144, 618468},  // default 353.7 us, chosen 169.6 us
 };
 
 inline constexpr PrefillGemmTable kPrefillGemmTables[] = {

@@ -583,14 +583,15 @@ def test_model_tuned_gemm_solutions_match_default(rt, model_dir, tmp_path):
     """The prefill projections' tuned rocBLAS solutions (prefill_gemm_table.h)
     against rocBLAS's default heuristic (MC_PREFILL_GEMM_DEFAULT=1, read once,
     so in a child process): the last-row logits of prefills whose row counts
-    select tuned rows (300 rows: the 256-row gate_up row; 8448 rows, one full
-    chunk: gate_up and down) agree to the logits tolerance. Only the GEMMs'
+    select tuned rows (300 rows: the 256-row gate_up row; 6200 rows: the
+    6144-row gate_up row; 8448 rows, one full chunk: gate_up and down) agree
+    to the logits tolerance. Only the GEMMs'
     summation order differs."""
     import json
     import subprocess
     import sys
     path, _ = model_dir
-    sizes = [300, 8448]
+    sizes = [300, 6200, 8448]
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     out = {}
     for tag, extra in (("tuned", {}), ("default", {"MC_PREFILL_GEMM_DEFAULT": "1"})):
