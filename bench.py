@@ -570,8 +570,9 @@ def bench_model(pkg, torch, steps):
     random bf16 weights (even / odd layers share one weight set, embedding
     and lm_head one table; the device holds every section separately, 5.03 GB)
     loaded through mc_model_load with HIP graphs; 2048- and 8448-token
-    prefills (the latter one full prefill chunk), solo decode after the
-    2048-token prompt and 8-session batch steps. Each decode streams every
+    prefills (the latter one full prefill chunk), 8-, 16- and 32-token ones
+    (best of 5), solo decode after the 2048-token prompt and 8-session batch
+    steps. Each decode streams every
     layer weight and the lm_head once: 4.50 GB per step."""
     import importlib
     import shutil
@@ -600,6 +601,21 @@ def bench_model(pkg, torch, steps):
         t0 = time.perf_counter()
         s.prefill(prompt)
         prefill_s = time.perf_counter() - t0
+        # short prompts (projections as row-group GEMVs up to 16 tokens)
+        short = {}
+        for n in (8, 16, 32):
+            s.reset()
+            s.prefill(prompt[:n])
+            ts = []
+            for _ in range(5):
+                s.reset()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                s.prefill(prompt[:n])
+                ts.append(time.perf_counter() - t0)
+            short[n] = min(ts)
+        s.reset()
+        s.prefill(prompt)
         for _ in range(3):
             s.decode_one(cfg)
         t0 = time.perf_counter()
@@ -660,6 +676,8 @@ def bench_model(pkg, torch, steps):
         "weights": "random bf16, full MiniCPM5-2B geometry (42 layers, vocab 130560)",
         "load_s": load_s, "weight_bytes_per_step": weight_bytes,
         "prefill_2048_ms": prefill_s * 1e3, "prefill_tokens_per_s": 2048 / prefill_s,
+        "prefill_8_ms": short[8] * 1e3, "prefill_16_ms": short[16] * 1e3,
+        "prefill_32_ms": short[32] * 1e3,
         "prefill_8448_ms": prefill_long_s * 1e3,
         "prefill_8448_tokens_per_s": 8448 / prefill_long_s,
         "decode_ms_per_token": solo * 1e3, "decode_tokens_per_s": 1.0 / solo,

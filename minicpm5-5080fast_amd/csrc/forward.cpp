@@ -307,6 +307,112 @@ void forward_carve(Forward& f, char* p, uint32_t rows, uint32_t logit_rows) {
     f.rows = rows;
 }
 
+// MC_PREFILL_ROWS_GEMV_OFF=1 sends chunks of 2..16 tokens through the GEMM
+// path as well (the measured A/B of forward_prefill_rows).
+bool prefill_rows_gemv_off() {
+    static const bool off = std::getenv("MC_PREFILL_ROWS_GEMV_OFF") != nullptr;
+    return off;
+}
+// Largest chunk taking the row-GEMV path: two launches of
+// MC_MODEL_GEMV_MAX_ROWS rows per projection. Measured (whole model, 42
+// layers): 9-16 tokens 3.22-3.57 ms against 3.62-3.87 through rocBLAS, 24
+// tokens 4.88 against 3.81 (every launch streams the weights from HBM: its
+// loads are non-temporal).
+constexpr uint32_t kPrefillRowsMax = 2u * MC_MODEL_GEMV_MAX_ROWS;
+
+// A prefill chunk of 2..kPrefillRowsMax tokens: the projections as M-row
+// GEMVs over groups of up to MC_MODEL_GEMV_MAX_ROWS rows (each weight byte
+// read once per group, the residual add + RMSNorm as their prologue, the
+// SwiGLU as the gate_up epilogue; the batch step's kernels), the RoPE append
+// and the prefill attention of the GEMM path, the lm_head on the last row. The same forward as the GEMM path up to
+// the projections' fp32 summation order (reference: forward.cpp:200-420
+// runs every T > 1 chunk through its GEMMs). The residual is kept as
+// cur + pending as in forward_decode.
+mc_status_t forward_prefill_rows(const Forward& f, const int32_t* d_ids, uint32_t n,
+                                 int32_t* d_next) {
+    TraceRange trace_range("forward_prefill_rows");
+    const ModelWeights& w = *f.w;
+    hipStream_t st = f.st;
+    const size_t last = (size_t)(n - 1u) * kHidden;  // the last row's offset
+    uint16_t* cur = f.res_a;
+    uint16_t* other = f.res_b;
+    const uint16_t* pending = nullptr;
+    const bool step_dump = dump_due(f.dump_step);
+    const bool layer_dump = step_dump && f.dump_layers;
+    const uint32_t S = mc_kv_prefill_split_kv(n);
+    constexpr uint32_t G = MC_MODEL_GEMV_MAX_ROWS;  // rows per GEMV launch
+    FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, cur, kHidden, n, st));
+    for (uint32_t l = 0; l < kModelLayers; ++l) {
+        if (layer_dump) {
+            FWD_OR_RETURN(residual_row(cur + last, pending ? pending + last : nullptr, f.attn,
+                                       w.norm1[l], f.normed, st));
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "hidden_in.f32"), f.attn, kHidden, st));
+        }
+        uint16_t* res_out = pending != nullptr ? other : nullptr;
+        for (uint32_t r = 0; r < n; r += G) {
+            const uint32_t m = std::min(G, n - r);
+            const size_t o = (size_t)r * kHidden;
+            FWD_OR_RETURN(mc_model_gemv_resnorm(
+                w.qkv[l], cur + o, pending ? pending + o : nullptr, w.norm1[l],
+                res_out ? res_out + o : nullptr, kHidden, f.qkv + (size_t)r * kQkvCols,
+                kQkvCols, m, kQkvCols, kRmsEps, st));
+        }
+        if (pending != nullptr) std::swap(cur, other);
+        FWD_OR_RETURN(mc_kv_rope_append(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout, kTheta,
+                                        rope_table_off() ? nullptr : f.inv_freq, st));
+        FWD_OR_RETURN(mc_kv_attention_prefill(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
+                                              f.attn, S > 1u ? f.pf_partials : nullptr, S, st));
+        for (uint32_t r = 0; r < n; r += G) {
+            const uint32_t m = std::min(G, n - r);
+            const size_t o = (size_t)r * kHidden;
+            FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn + o, kHidden, f.o_out + o, kHidden, m,
+                                        kHidden, kHidden, st));
+        }
+        for (uint32_t r = 0; r < n; r += G) {
+            const uint32_t m = std::min(G, n - r);
+            const size_t o = (size_t)r * kHidden;
+            FWD_OR_RETURN(mc_model_gemv_resnorm_swiglu(w.gate_up[l], cur + o, f.o_out + o,
+                                                       w.norm2[l], other + o, kHidden,
+                                                       f.mlp + (size_t)r * kInter, kInter, m,
+                                                       kInter, kRmsEps, st));
+        }
+        std::swap(cur, other);
+        for (uint32_t r = 0; r < n; r += G) {
+            const uint32_t m = std::min(G, n - r);
+            FWD_OR_RETURN(mc_model_gemv(w.down[l], f.mlp + (size_t)r * kInter, kInter,
+                                        f.down + (size_t)r * kHidden, kHidden, m, kHidden,
+                                        kInter, st));
+        }
+        pending = f.down;
+        if (layer_dump) {  // cur: the residual after the o projection
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "attn_out.f32"), cur + last, kHidden,
+                                    st));
+            FWD_OR_RETURN(residual_row(cur + last, pending + last, f.attn, w.norm1[0], f.normed,
+                                       st));
+            FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "mlp_out.f32"), f.attn, kHidden, st));
+        }
+    }
+    if (step_dump) {  // final_hidden = final_norm(cur + pending), last row
+        FWD_OR_RETURN(residual_row(cur + last, pending + last, f.attn, w.final_norm, f.normed,
+                                   st));
+        FWD_OR_RETURN(mc_model_rmsnorm_rows(f.attn, nullptr, w.final_norm, f.normed, 1, kHidden,
+                                            kRmsEps, st));
+        FWD_OR_RETURN(dump_bf16(dump_name("step", f.dump_step, "final_hidden.f32"), f.normed,
+                                kHidden, st));
+    }
+    FWD_OR_RETURN(mc_model_gemv_resnorm(w.lm_head, cur + last, pending + last, w.final_norm,
+                                        nullptr, kHidden, f.logits, kVocabSize, 1, kVocabSize,
+                                        kRmsEps, st));
+    FWD_OR_RETURN(mc_model_argmax_bf16(f.logits, kVocabSize, 1, d_next, nullptr, f.stage_v,
+                                       f.stage_i, st));
+    if (step_dump) {
+        FWD_OR_RETURN(dump_bf16(dump_name("step", f.dump_step, "logits.f32"), f.logits,
+                                kVocabSize, st));
+        FWD_OR_RETURN(dump_token(dump_name("step", f.dump_step, "token"), d_next, st));
+    }
+    return MC_OK;
+}
+
 mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, int32_t* d_next) {
     TraceRange trace_range("forward_prefill");
     const ModelWeights& w = *f.w;
@@ -320,6 +426,8 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
     // decode attention and the FP8 lm_head: forward.cpp:117-130,252-282,
     // 444-456), not through the GEMMs and prefill attention.
     if (n == 1u) return forward_decode(f, d_ids, d_next, Marker{});
+    if (n <= kPrefillRowsMax && !prefill_rows_gemv_off())
+        return forward_prefill_rows(f, d_ids, n, d_next);
     uint16_t* res = f.res_a;
     const bool step_dump = dump_due(f.dump_step);
     const bool layer_dump = step_dump && f.dump_layers;

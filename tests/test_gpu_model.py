@@ -513,7 +513,9 @@ m.close()
 """
 
 
-def test_model_debug_dump_files(rt, orc, model_dir, tmp_path):
+@pytest.mark.parametrize("prompt", [[1, 500, 130559, 77, 9, 12345, 3, 3, 42],
+                                    [1, 500, 130559, 77, 9]])
+def test_model_debug_dump_files(rt, orc, model_dir, tmp_path, prompt):
     """The reference's debug dump (debug_dump.h:1-12; MC_DEBUG_DUMP_DIR and
     MC_DEBUG_DUMP_STEPS, read once, so a child process runs the session):
     forwards 0..N-1 (the prefill, then each decode) write step{t}.logits /
@@ -521,7 +523,8 @@ def test_model_debug_dump_files(rt, orc, model_dir, tmp_path):
     mlp_out (last row, bf16 widened to fp32). The files equal the session's
     own logits and tokens, and the layer rows and final rows match the
     oracle's within the logits tolerance. Decode steps that dump run
-    eagerly under a graph-enabled model."""
+    eagerly under a graph-enabled model. A 9-token prompt runs the GEMM
+    prefill, a 5-token one the row-GEMV prefill."""
     import json
     import subprocess
     import sys
@@ -529,7 +532,6 @@ def test_model_debug_dump_files(rt, orc, model_dir, tmp_path):
     path, w = model_dir
     d = tmp_path / "dump"
     d.mkdir()
-    prompt = [1, 500, 130559, 77, 9, 12345, 3, 3, 42]
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     env = dict(os.environ, MC_DEBUG_DUMP_DIR=str(d), MC_DEBUG_DUMP_STEPS="3")
     r = subprocess.run([sys.executable, "-c", _DUMP_CHILD, root, path, str(d),
@@ -610,6 +612,91 @@ def test_model_tuned_gemm_solutions_match_default(rt, model_dir, tmp_path):
         rel, cos = compare_logits(out["tuned"][2 * i], out["default"][2 * i])
         print("rows", n, "rel", rel, "cos", cos)
         assert rel < 2e-2 and cos > 0.999, n
+
+
+_ROWS_CHILD = r"""
+import importlib, json, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+rt = importlib.import_module("minicpm5-5080fast_amd.runtime")
+m = rt.Model(sys.argv[2], rt.model_options(max_context_tokens=4096, max_sessions=1))
+s = rt.Session(m)
+out = []
+for p in json.loads(sys.argv[4]):
+    s.reset()
+    s.prefill(p)
+    out.append(s.last_logits())
+np.save(sys.argv[3], np.stack(out))
+s.close()
+m.close()
+"""
+
+
+def test_model_short_prefill_rows_path(rt, orc, model_dir, tmp_path):
+    """Prefill chunks of 2..16 tokens run their projections as GEMVs over
+    groups of up to 8 rows (forward_prefill_rows). Their last-row logits
+    match the oracle's forward, the greedy continuation matches the oracle's
+    decode, and they agree with the GEMM path (MC_PREFILL_ROWS_GEMV_OFF=1,
+    read once, so in a child process) to the logits tolerance. A prompt
+    prefilled as a 20-token call (GEMM path) and a 5-token call (row path)
+    gives the same logits on two sessions and matches the oracle."""
+    import json
+    import subprocess
+    import sys
+    from oracle import model_ref as R
+    path, w = model_dir
+    prompts = [[7, 130000], [1, 500, 130559, 77, 9], [11 * i + 3 for i in range(8)],
+               [(13 * i + 5) % 130560 for i in range(13)], [17 * i for i in range(16)]]
+    m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2))
+    s = rt.Session(m)
+    got = []
+    cfg = rt.gen_config(max_new_tokens=8)
+    for p in prompts:
+        s.reset()
+        s.prefill(p)
+        got.append(s.last_logits())
+        ref = R.ModelRef(w, 42)
+        ref.forward(p)
+        rel, cos = compare_logits(got[-1], ref.last_logits)
+        print(len(p), "rows: oracle rel", rel, "cos", cos)
+        assert rel < 2e-2 and cos > 0.999, (len(p), rel, cos)
+        for step in range(2):
+            tok = s.decode_one(cfg)
+            if clear_winner(ref.last_logits):
+                assert tok == ref.next_token, (len(p), step, tok, ref.next_token)
+            ref.next_token = tok
+            ref.decode()
+            rel, cos = compare_logits(s.last_logits(), ref.last_logits)
+            assert rel < 2e-2 and cos > 0.999, (len(p), step, rel, cos)
+    s.close()
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    f = str(tmp_path / "gemm.npy")
+    env = dict(os.environ, MC_PREFILL_ROWS_GEMV_OFF="1")
+    r = subprocess.run([sys.executable, "-c", _ROWS_CHILD, root, path, f, json.dumps(prompts)],
+                       env=env, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-3000:]
+    gemm = np.load(f)
+    for i, p in enumerate(prompts):
+        rel, cos = compare_logits(got[i], gemm[i])
+        print(len(p), "rows: GEMM path rel", rel, "cos", cos)
+        assert rel < 2e-2 and cos > 0.999, (len(p), rel, cos)
+    # a 5-token call after a 20-token one (GEMM path) continues the same session
+    # state
+    a, b = rt.Session(m), rt.Session(m)
+    long_p = [(i * 7919 + 1) % 130560 for i in range(25)]
+    a.prefill(long_p[:20])
+    a.prefill(long_p[20:])
+    b.prefill(long_p[:20])
+    b.prefill(long_p[20:])
+    assert np.array_equal(a.last_logits(), b.last_logits())
+    ref = R.ModelRef(w, 42)
+    ref.forward(long_p[:20])
+    ref.forward(long_p[20:])
+    rel, cos = compare_logits(a.last_logits(), ref.last_logits)
+    assert rel < 2e-2 and cos > 0.999, (rel, cos)
+    a.close()
+    b.close()
+    m.close()
 
 
 def test_model_seed_residual_hook(rt, model_dir, tmp_path):
