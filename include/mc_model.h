@@ -90,6 +90,23 @@ mc_status_t mc_model_gemv_swiglu(const uint16_t* d_w, const uint16_t* d_gate_up,
                                  uint16_t* d_y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
                                  void* stream);
 
+/* Row GEMM of a prefill chunk of MC_MODEL_GEMM_ROWS_MIN..MAX rows: d_y[m][n] =
+ * bf16(sum_k d_w[n][k] * d_x[m][k]) with fp32 accumulation (swiglu = 0), or,
+ * with swiglu = 1, d_y[m][n] = bf16(silu(g) * u) where g and u are the rows
+ * n and N + n of d_w ([2N][K]: gate rows, then up rows) dotted with x_m and
+ * rounded to bf16 (the gate_up projection followed by the SwiGLU, as
+ * mc_model_gemv_resnorm_swiglu). N a multiple of 16, K 2048 or 6144 (2048
+ * with swiglu), row
+ * strides ldx (multiple of 8) and ldy (multiple of 4) in elements. No
+ * reference counterpart: the reference runs every multi-token chunk through
+ * cuBLAS (forward.cpp:200-420); this replaces the library GEMM where its
+ * per-call cost dominates. */
+#define MC_MODEL_GEMM_ROWS_MIN 9u
+#define MC_MODEL_GEMM_ROWS_MAX 32u
+mc_status_t mc_model_gemm_rows(const uint16_t* d_w, const uint16_t* d_x, uint32_t ldx,
+                               uint16_t* d_y, uint32_t ldy, uint32_t M, uint32_t N, uint32_t K,
+                               uint32_t swiglu, void* stream);
+
 /* ---- FP8 projections (precision MC_FP8: single-token forwards) ----
  * d_w: e4m3 codes [N][K] (uint8, 16-byte aligned rows), d_scale: fp32 [N]
  * row scales; d_y[n] = bf16(d_scale[n] * sum_k e4m3(d_w[n][k]) * x[k])

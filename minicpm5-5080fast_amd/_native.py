@@ -86,6 +86,7 @@ _SIGS = {
     "mc_model_rmsnorm_rows": (C.c_int, [_P, _P, _P, _P, _u32, _u32, C.c_float, _P]),
     "mc_model_swiglu_rows": (C.c_int, [_P, _P, _u32, _u32, _P]),
     "mc_model_gemv": (C.c_int, [_P, _P, _u32, _P, _u32, _u32, _u32, _u32, _P]),
+    "mc_model_gemm_rows": (C.c_int, [_P, _P, _u32, _P, _u32, _u32, _u32, _u32, _u32, _P]),
     "mc_model_gemv_resnorm": (C.c_int, [_P, _P, _P, _P, _P, _u32, _P, _u32, _u32, _u32,
                                         C.c_float, _P]),
     "mc_model_gemv_swiglu": (C.c_int, [_P, _P, _u32, _P, _u32, _u32, _u32, _u32, _P]),

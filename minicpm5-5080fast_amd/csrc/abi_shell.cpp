@@ -219,7 +219,7 @@ struct SessionImpl {
     Breakdown bd;
     // with weights
     Forward fwd;
-    rocblas_handle blas = nullptr;
+    void* blas = nullptr;  // prefill GEMM libraries (prefill_blas_create)
     int32_t* h_emit = nullptr;  // pinned: the token a decode returns
 };
 
@@ -306,7 +306,7 @@ void release_session(SessionImpl* s) {
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     destroy_graph(s->step_graph);
     s->bd.destroy();
-    if (s->blas) (void)rocblas_destroy_handle(s->blas);
+    prefill_blas_destroy(s->blas);
     if (s->h_emit) (void)hipHostFree(s->h_emit);
     if (s->kv) mc_kv_allocator_destroy(s->kv);
     if (s->arena) (void)hipFree(s->arena);
@@ -546,13 +546,11 @@ mc_status_t mc_session_create(mc_model_t model, mc_session_t* out_session) {
     s->max_chunks = mc_kv_decode_max_chunks(m->max_ctx, s->chunk_pos);
     s->act_rows = std::min(m->max_ctx, prefill_chunk_tokens());
     const size_t pool_b = (size_t)mc_kv_total_elems(s->layout) * 2u;
-    // With weights: the prefill projections' rocBLAS handle gets its device
-    // workspace from the arena, so rocBLAS never allocates after create.
+    // With weights: the prefill projections' rocBLAS and hipBLASLt handles get
+    // their device workspace from the arena, so neither allocates after create.
     size_t blas_ws = 0;
     if (m->weights) {
-        void* bh = nullptr;
-        const mc_status_t bs = prefill_blas_create(&bh, &blas_ws);
-        s->blas = static_cast<rocblas_handle>(bh);
+        const mc_status_t bs = prefill_blas_create(&s->blas, &blas_ws);
         if (bs != MC_OK) {
             release_session(s);
             return bs;

@@ -26,6 +26,7 @@
 //     workgroups still reading the old one. Attention is the phase0 decode
 //     (RoPE + K/V append + split-KV attention in one chunk kernel).
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
@@ -34,7 +35,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <new>
 #include <string>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -70,9 +74,14 @@ size_t a256(size_t x) { return (x + 255u) & ~size_t(255); }
 
 // The tuned table of the rocBLAS this process resolved (by its version
 // string), or null.
+bool gemm_defaults_only() {
+    static const bool on = std::getenv("MC_PREFILL_GEMM_DEFAULT") != nullptr;
+    return on;
+}
+
 const PrefillGemmTable* gemm_table() {
     static const PrefillGemmTable* t = []() -> const PrefillGemmTable* {
-        if (std::getenv("MC_PREFILL_GEMM_DEFAULT") != nullptr) return nullptr;
+        if (gemm_defaults_only()) return nullptr;
         char ver[256] = {0};
         if (rocblas_get_version_string(ver, sizeof(ver)) != rocblas_status_success)
             return nullptr;
@@ -99,37 +108,124 @@ int gemm_row(const PrefillGemmTable* t, uint32_t M, uint32_t N, uint32_t K) {
     return row;
 }
 
-// y[M][N] = x[M][K] . W[N][K]^T through rocBLAS (column-major view: C(N x M) =
-// W^T(N x K) . x^T(K x M)), with the tuned solution of the shape. An index
-// that rocBLAS rejects (it checks one against the problem before launching)
-// reruns the call on the default heuristic and leaves that table row on it
-// for the rest of the process, as MC_PREFILL_GEMM_DEFAULT=1 does for every
-// row (the measured A/B of the tables).
+// The prefill projections' GEMM libraries of one session.
+struct PrefillBlas {
+    rocblas_handle rb = nullptr;
+    hipblasLtHandle_t lt = nullptr;
+    hipblasLtMatmulDesc_t desc = nullptr;  // y^T = W^T(op T) . x^T, fp32 compute
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+// hipBLASLt rows: chunks of kLtMinRows..kLtMaxRows rows without a tuned
+// rocBLAS solution go through hipBLASLt with the heuristic's first algorithm,
+// looked up once per (M, N, K) per process. Through PyTorch's libraries a
+// rocblas_gemm_ex call takes ~16 us of host time whatever the size, a
+// hipblasLtMatmul call ~9 us; below ~1024 rows the GPU finishes a projection
+// sooner than that, so the host sets the prefill's pace. Larger chunks stay
+// on rocBLAS (unchanged kernels; the host time is hidden there).
+constexpr uint32_t kLtMinRows = 17u, kLtMaxRows = 1023u;
+
+struct LtAlgoCache {
+    std::mutex mu;
+    std::unordered_map<uint64_t, hipblasLtMatmulAlgo_t> algos;
+    std::unordered_map<uint64_t, bool> failed;
+};
+LtAlgoCache& lt_cache() {
+    static LtAlgoCache c;
+    return c;
+}
+
+// y[M][N] = x[M][K] . W[N][K]^T through hipBLASLt; false (nothing launched)
+// when hipBLASLt has no algorithm for the shape or rejects the call.
+bool gemm_lt(const PrefillBlas& b, hipStream_t st, const uint16_t* x, uint32_t M,
+             const uint16_t* W, uint32_t N, uint32_t K, uint16_t* y) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    const uint64_t key = ((uint64_t)(uint32_t)dev << 56) ^ ((uint64_t)M << 32) ^
+                         ((uint64_t)N << 16) ^ (uint64_t)K;
+    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+    bool ok = hipblasLtMatrixLayoutCreate(&la, HIP_R_16BF, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&lb, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&lc, HIP_R_16BF, N, M, N) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulAlgo_t algo{};
+    if (ok) {
+        LtAlgoCache& c = lt_cache();
+        std::lock_guard<std::mutex> lk(c.mu);
+        auto it = c.algos.find(key);
+        if (it != c.algos.end()) {
+            algo = it->second;
+        } else if (c.failed.count(key)) {
+            ok = false;
+        } else {
+            hipblasLtMatmulPreference_t pref = nullptr;
+            hipblasLtMatmulHeuristicResult_t res{};
+            int n = 0;
+            uint64_t wsz = b.ws_bytes;
+            ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatmulPreferenceSetAttribute(
+                     pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof(wsz)) ==
+                     HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatmulAlgoGetHeuristic(b.lt, b.desc, la, lb, lc, lc, pref, 1, &res,
+                                                 &n) == HIPBLAS_STATUS_SUCCESS &&
+                 n > 0 && res.state == HIPBLAS_STATUS_SUCCESS && res.workspaceSize <= b.ws_bytes;
+            if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+            if (ok) {
+                algo = res.algo;
+                c.algos.emplace(key, algo);
+            } else {
+                c.failed.emplace(key, true);
+            }
+        }
+    }
+    if (ok) {
+        const float alpha = 1.f, beta = 0.f;
+        ok = hipblasLtMatmul(b.lt, b.desc, &alpha, W, la, x, lb, &beta, y, lc, y, lc, &algo, b.ws,
+                             b.ws_bytes, st) == HIPBLAS_STATUS_SUCCESS;
+    }
+    if (la) (void)hipblasLtMatrixLayoutDestroy(la);
+    if (lb) (void)hipblasLtMatrixLayoutDestroy(lb);
+    if (lc) (void)hipblasLtMatrixLayoutDestroy(lc);
+    return ok;
+}
+
+// y[M][N] = x[M][K] . W[N][K]^T (column-major view: C(N x M) = W^T(N x K) .
+// x^T(K x M)). A shape with a tuned rocBLAS solution runs it; an index that
+// rocBLAS rejects (it checks one against the problem before launching) reruns
+// the call on the default heuristic and leaves that table row on it for the
+// rest of the process. Other shapes of kLtMinRows..kLtMaxRows rows go through
+// hipBLASLt, the rest (and whatever hipBLASLt declines) through rocBLAS's
+// default heuristic. MC_PREFILL_GEMM_DEFAULT=1 sends every projection to
+// rocBLAS's default heuristic (the measured A/B of the tables and the
+// hipBLASLt rows).
 mc_status_t gemm_bf16(const Forward& f, const uint16_t* x, uint32_t M, const uint16_t* W,
                       uint32_t N, uint32_t K, uint16_t* y) {
-    rocblas_handle h = static_cast<rocblas_handle>(f.blas);
-    if (rocblas_set_stream(h, f.st) != rocblas_status_success) {
-        set_error("prefill GEMM: rocblas_set_stream failed");
-        return MC_E_CUDA;
-    }
-    const float alpha = 1.f, beta = 0.f;
-    auto run = [&](int32_t idx) {
-        return rocblas_gemm_ex(
-            h, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)N,
-            (rocblas_int)M, (rocblas_int)K, &alpha, W, rocblas_datatype_bf16_r, (rocblas_int)K, x,
-            rocblas_datatype_bf16_r, (rocblas_int)K, &beta, y, rocblas_datatype_bf16_r,
-            (rocblas_int)N, y, rocblas_datatype_bf16_r, (rocblas_int)N, rocblas_datatype_f32_r,
-            idx ? rocblas_gemm_algo_solution_index : rocblas_gemm_algo_standard, idx, 0);
-    };
+    const PrefillBlas& b = *static_cast<const PrefillBlas*>(f.blas);
     const PrefillGemmTable* t = gemm_table();
     const int row = gemm_row(t, M, N, K);
-    // rows whose index this process's rocBLAS rejected (it validates an index
-    // before launching anything)
+    // rows whose index this process's rocBLAS rejected
     static std::atomic<uint64_t> rejected{0};
     const uint64_t bit = row >= 0 ? uint64_t(1) << row : 0u;
     const int32_t idx = row >= 0 && !(rejected.load(std::memory_order_relaxed) & bit)
                             ? t->rows[row].index
                             : 0;
+    if (idx == 0 && M >= kLtMinRows && M <= kLtMaxRows && !gemm_defaults_only() &&
+        gemm_lt(b, f.st, x, M, W, N, K, y))
+        return MC_OK;
+    rocblas_handle h = b.rb;
+    if (rocblas_set_stream(h, f.st) != rocblas_status_success) {
+        set_error("prefill GEMM: rocblas_set_stream failed");
+        return MC_E_CUDA;
+    }
+    const float alpha = 1.f, beta = 0.f;
+    auto run = [&](int32_t i) {
+        return rocblas_gemm_ex(
+            h, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)N,
+            (rocblas_int)M, (rocblas_int)K, &alpha, W, rocblas_datatype_bf16_r, (rocblas_int)K, x,
+            rocblas_datatype_bf16_r, (rocblas_int)K, &beta, y, rocblas_datatype_bf16_r,
+            (rocblas_int)N, y, rocblas_datatype_bf16_r, (rocblas_int)N, rocblas_datatype_f32_r,
+            i ? rocblas_gemm_algo_solution_index : rocblas_gemm_algo_standard, i, 0);
+    };
     rocblas_status s = run(idx);
     if (s != rocblas_status_success && idx != 0) {
         rejected.fetch_or(bit, std::memory_order_relaxed);
@@ -252,24 +348,53 @@ bool dump_due(uint32_t step) {
 mc_status_t prefill_blas_create(void** out, size_t* ws_bytes) {
     *out = nullptr;
     *ws_bytes = kBlasWorkspace;
-    rocblas_handle h = nullptr;
-    if (rocblas_create_handle(&h) != rocblas_status_success) {
+    PrefillBlas* b = new (std::nothrow) PrefillBlas;
+    if (b == nullptr) {
+        set_error("mc_session_create: out of host memory");
+        return MC_E_OUT_OF_MEMORY;
+    }
+    if (rocblas_create_handle(&b->rb) != rocblas_status_success) {
+        b->rb = nullptr;
+        prefill_blas_destroy(b);
         set_error("mc_session_create: rocblas_create_handle failed");
         return MC_E_CUDA;
     }
-    *out = h;
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    if (hipblasLtCreate(&b->lt) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescCreate(&b->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) !=
+            HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(b->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) !=
+            HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(b->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) !=
+            HIPBLAS_STATUS_SUCCESS) {
+        prefill_blas_destroy(b);
+        set_error("mc_session_create: hipBLASLt handle or matmul descriptor creation failed");
+        return MC_E_CUDA;
+    }
+    *out = b;
     return MC_OK;
 }
 
 mc_status_t prefill_blas_workspace(void* hv, void* ws, size_t ws_bytes) {
-    rocblas_handle h = static_cast<rocblas_handle>(hv);
-    const rocblas_status st = rocblas_set_workspace(h, ws, ws_bytes);
+    PrefillBlas* b = static_cast<PrefillBlas*>(hv);
+    const rocblas_status st = rocblas_set_workspace(b->rb, ws, ws_bytes);
     if (st != rocblas_status_success) {
         set_error("mc_session_create: rocblas_set_workspace failed: %s",
                   rocblas_status_to_string(st));
         return MC_E_CUDA;
     }
+    b->ws = ws;  // hipBLASLt takes it per call
+    b->ws_bytes = ws_bytes;
     return MC_OK;
+}
+
+void prefill_blas_destroy(void* hv) {
+    PrefillBlas* b = static_cast<PrefillBlas*>(hv);
+    if (b == nullptr) return;
+    if (b->desc) (void)hipblasLtMatmulDescDestroy(b->desc);
+    if (b->lt) (void)hipblasLtDestroy(b->lt);
+    if (b->rb) (void)rocblas_destroy_handle(b->rb);
+    delete b;
 }
 
 size_t forward_act_bytes(uint32_t rows, uint32_t logit_rows) {
@@ -307,24 +432,23 @@ void forward_carve(Forward& f, char* p, uint32_t rows, uint32_t logit_rows) {
     f.rows = rows;
 }
 
-// MC_PREFILL_ROWS_GEMV_OFF=1 sends chunks of 2..16 tokens through the GEMM
-// path as well (the measured A/B of forward_prefill_rows).
+// Projections of short prefill chunks (whole model, 42 layers, best of 5;
+// library GEMMs in parentheses): 2..8 tokens through forward_prefill_rows
+// 1.74-2.16 ms (3.60-3.67), 9..32 tokens through the row GEMM 2.45-3.31 ms
+// (3.30-3.74); at 33-64 tokens the row GEMM measured slower than hipBLASLt
+// (its activation reads grow with the rows on each of the N / 16
+// workgroups). MC_PREFILL_ROWS_GEMV_OFF=1 sends chunks of 2..32 tokens
+// through the GEMM libraries as well (the measured A/B).
 bool prefill_rows_gemv_off() {
     static const bool off = std::getenv("MC_PREFILL_ROWS_GEMV_OFF") != nullptr;
     return off;
 }
-// Largest chunk taking the row-GEMV path: two launches of
-// MC_MODEL_GEMV_MAX_ROWS rows per projection. Measured (whole model, 42
-// layers): 9-16 tokens 3.22-3.57 ms against 3.62-3.87 through rocBLAS, 24
-// tokens 4.88 against 3.81 (every launch streams the weights from HBM: its
-// loads are non-temporal).
-constexpr uint32_t kPrefillRowsMax = 2u * MC_MODEL_GEMV_MAX_ROWS;
 
-// A prefill chunk of 2..kPrefillRowsMax tokens: the projections as M-row
-// GEMVs over groups of up to MC_MODEL_GEMV_MAX_ROWS rows (each weight byte
-// read once per group, the residual add + RMSNorm as their prologue, the
-// SwiGLU as the gate_up epilogue; the batch step's kernels), the RoPE append
-// and the prefill attention of the GEMM path, the lm_head on the last row. The same forward as the GEMM path up to
+// A prefill chunk of 2..MC_MODEL_GEMV_MAX_ROWS tokens: the projections as
+// M-row GEMVs (each weight byte read once for all rows, the residual add +
+// RMSNorm as their prologue, the SwiGLU as the gate_up epilogue; the batch
+// step's kernels), the RoPE append and the prefill attention of the GEMM
+// path, the lm_head on the last row. The same forward as the GEMM path up to
 // the projections' fp32 summation order (reference: forward.cpp:200-420
 // runs every T > 1 chunk through its GEMMs). The residual is kept as
 // cur + pending as in forward_decode.
@@ -340,7 +464,6 @@ mc_status_t forward_prefill_rows(const Forward& f, const int32_t* d_ids, uint32_
     const bool step_dump = dump_due(f.dump_step);
     const bool layer_dump = step_dump && f.dump_layers;
     const uint32_t S = mc_kv_prefill_split_kv(n);
-    constexpr uint32_t G = MC_MODEL_GEMV_MAX_ROWS;  // rows per GEMV launch
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, cur, kHidden, n, st));
     for (uint32_t l = 0; l < kModelLayers; ++l) {
         if (layer_dump) {
@@ -349,40 +472,21 @@ mc_status_t forward_prefill_rows(const Forward& f, const int32_t* d_ids, uint32_
             FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "hidden_in.f32"), f.attn, kHidden, st));
         }
         uint16_t* res_out = pending != nullptr ? other : nullptr;
-        for (uint32_t r = 0; r < n; r += G) {
-            const uint32_t m = std::min(G, n - r);
-            const size_t o = (size_t)r * kHidden;
-            FWD_OR_RETURN(mc_model_gemv_resnorm(
-                w.qkv[l], cur + o, pending ? pending + o : nullptr, w.norm1[l],
-                res_out ? res_out + o : nullptr, kHidden, f.qkv + (size_t)r * kQkvCols,
-                kQkvCols, m, kQkvCols, kRmsEps, st));
-        }
+        FWD_OR_RETURN(mc_model_gemv_resnorm(w.qkv[l], cur, pending, w.norm1[l], res_out, kHidden,
+                                            f.qkv, kQkvCols, n, kQkvCols, kRmsEps, st));
         if (pending != nullptr) std::swap(cur, other);
         FWD_OR_RETURN(mc_kv_rope_append(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout, kTheta,
                                         rope_table_off() ? nullptr : f.inv_freq, st));
         FWD_OR_RETURN(mc_kv_attention_prefill(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
                                               f.attn, S > 1u ? f.pf_partials : nullptr, S, st));
-        for (uint32_t r = 0; r < n; r += G) {
-            const uint32_t m = std::min(G, n - r);
-            const size_t o = (size_t)r * kHidden;
-            FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn + o, kHidden, f.o_out + o, kHidden, m,
-                                        kHidden, kHidden, st));
-        }
-        for (uint32_t r = 0; r < n; r += G) {
-            const uint32_t m = std::min(G, n - r);
-            const size_t o = (size_t)r * kHidden;
-            FWD_OR_RETURN(mc_model_gemv_resnorm_swiglu(w.gate_up[l], cur + o, f.o_out + o,
-                                                       w.norm2[l], other + o, kHidden,
-                                                       f.mlp + (size_t)r * kInter, kInter, m,
-                                                       kInter, kRmsEps, st));
-        }
+        FWD_OR_RETURN(mc_model_gemv(w.o[l], f.attn, kHidden, f.o_out, kHidden, n, kHidden,
+                                    kHidden, st));
+        FWD_OR_RETURN(mc_model_gemv_resnorm_swiglu(w.gate_up[l], cur, f.o_out, w.norm2[l], other,
+                                                   kHidden, f.mlp, kInter, n, kInter, kRmsEps,
+                                                   st));
         std::swap(cur, other);
-        for (uint32_t r = 0; r < n; r += G) {
-            const uint32_t m = std::min(G, n - r);
-            FWD_OR_RETURN(mc_model_gemv(w.down[l], f.mlp + (size_t)r * kInter, kInter,
-                                        f.down + (size_t)r * kHidden, kHidden, m, kHidden,
-                                        kInter, st));
-        }
+        FWD_OR_RETURN(mc_model_gemv(w.down[l], f.mlp, kInter, f.down, kHidden, n, kHidden, kInter,
+                                    st));
         pending = f.down;
         if (layer_dump) {  // cur: the residual after the o projection
             FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "attn_out.f32"), cur + last, kHidden,
@@ -426,7 +530,7 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
     // decode attention and the FP8 lm_head: forward.cpp:117-130,252-282,
     // 444-456), not through the GEMMs and prefill attention.
     if (n == 1u) return forward_decode(f, d_ids, d_next, Marker{});
-    if (n <= kPrefillRowsMax && !prefill_rows_gemv_off())
+    if (n <= MC_MODEL_GEMV_MAX_ROWS && !prefill_rows_gemv_off())
         return forward_prefill_rows(f, d_ids, n, d_next);
     uint16_t* res = f.res_a;
     const bool step_dump = dump_due(f.dump_step);
@@ -435,22 +539,35 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, res, kHidden, n, st));
     FWD_OR_RETURN(mc_model_rmsnorm_rows(res, nullptr, w.norm1[0], f.normed, n, kHidden, kRmsEps, st));
     const uint32_t S = mc_kv_prefill_split_kv(n);
+    // 9..32 rows: the projections through the row GEMM (the gate_up one with
+    // the SwiGLU as its epilogue), larger chunks through the GEMM libraries
+    const bool rows = n >= MC_MODEL_GEMM_ROWS_MIN && n <= MC_MODEL_GEMM_ROWS_MAX &&
+                      !prefill_rows_gemv_off();
+    auto proj = [&](const uint16_t* x, const uint16_t* W, uint32_t N, uint32_t K, uint16_t* y) {
+        return rows ? mc_model_gemm_rows(W, x, K, y, N, n, N, K, 0u, st)
+                    : gemm_bf16(f, x, n, W, N, K, y);
+    };
     for (uint32_t l = 0; l < kModelLayers; ++l) {
         if (layer_dump)
             FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "hidden_in.f32"), res_last, kHidden, st));
-        FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.qkv[l], kQkvCols, kHidden, f.qkv));
+        FWD_OR_RETURN(proj(f.normed, w.qkv[l], kQkvCols, kHidden, f.qkv));
         FWD_OR_RETURN(mc_kv_rope_append(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout, kTheta,
                                         rope_table_off() ? nullptr : f.inv_freq, st));
         FWD_OR_RETURN(mc_kv_attention_prefill(f.qkv, n, f.d_seq_len, l, f.d_pt, f.pool, f.layout,
                                               f.attn, S > 1u ? f.pf_partials : nullptr, S, st));
-        FWD_OR_RETURN(gemm_bf16(f, f.attn, n, w.o[l], kHidden, kHidden, f.o_out));
+        FWD_OR_RETURN(proj(f.attn, w.o[l], kHidden, kHidden, f.o_out));
         FWD_OR_RETURN(
             mc_model_rmsnorm_rows(res, f.o_out, w.norm2[l], f.normed, n, kHidden, kRmsEps, st));
         if (layer_dump)
             FWD_OR_RETURN(dump_bf16(dump_name("layer", l, "attn_out.f32"), res_last, kHidden, st));
-        FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.gate_up[l], 2u * kInter, kHidden, f.gate_up));
-        FWD_OR_RETURN(mc_model_swiglu_rows(f.gate_up, f.mlp, n, kInter, st));
-        FWD_OR_RETURN(gemm_bf16(f, f.mlp, n, w.down[l], kHidden, kInter, f.down));
+        if (rows) {
+            FWD_OR_RETURN(mc_model_gemm_rows(w.gate_up[l], f.normed, kHidden, f.mlp, kInter, n,
+                                             kInter, kHidden, 1u, st));
+        } else {
+            FWD_OR_RETURN(gemm_bf16(f, f.normed, n, w.gate_up[l], 2u * kInter, kHidden, f.gate_up));
+            FWD_OR_RETURN(mc_model_swiglu_rows(f.gate_up, f.mlp, n, kInter, st));
+        }
+        FWD_OR_RETURN(proj(f.mlp, w.down[l], kHidden, kInter, f.down));
         const uint16_t* next_norm = l + 1u < kModelLayers ? w.norm1[l + 1u] : w.final_norm;
         FWD_OR_RETURN(
             mc_model_rmsnorm_rows(res, f.down, next_norm, f.normed, n, kHidden, kRmsEps, st));

@@ -67,7 +67,7 @@ namespace mckv {
 struct Forward {
     const ModelWeights* w = nullptr;
     hipStream_t st = nullptr;
-    void* blas = nullptr;  // rocblas_handle for the prefill GEMMs
+    void* blas = nullptr;  // prefill GEMM libraries (prefill_blas_create)
     // KV cache of a session (prefill and solo decode)
     uint16_t* pool = nullptr;
     const uint32_t* d_pt = nullptr;
@@ -103,12 +103,15 @@ bool dump_due(uint32_t step);
 size_t forward_act_bytes(uint32_t rows, uint32_t logit_rows);
 void forward_carve(Forward& f, char* base, uint32_t rows, uint32_t logit_rows);
 
-// rocBLAS handle of a session's prefill projections and the size of the
+// GEMM library state of a session's prefill projections (a rocBLAS handle
+// and a hipBLASLt handle with its matmul descriptor) and the size of the
 // device workspace it is to be given (*ws_bytes); prefill_blas_workspace then
 // hands it that much caller memory (carved from the session arena), after
-// which rocBLAS allocates nothing. On failure *h is null.
+// which neither library allocates. On failure *h is null (and nothing is
+// held). prefill_blas_destroy(nullptr) does nothing.
 mc_status_t prefill_blas_create(void** h, size_t* ws_bytes);
 mc_status_t prefill_blas_workspace(void* h, void* ws, size_t ws_bytes);
+void prefill_blas_destroy(void* h);
 
 // Prefill of n <= rows tokens at positions *d_seq_len.. (ids on the device):
 // K/V of every layer appended, the greedy next token written to *d_next.

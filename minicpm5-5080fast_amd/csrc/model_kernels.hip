@@ -782,6 +782,128 @@ bool launch_gemv_m(uint32_t M, const GemvArgs& a, hipStream_t st) {
     }
 }
 
+// ---- row GEMM for prefill chunks of MC_MODEL_GEMM_ROWS_MIN..MAX rows ----
+// y[m][n] = bf16(sum_k W[n][k] x[m][k]) (or, SWI, bf16(silu(g) * u) of the
+// gate row n and up row N + n, each rounded to bf16 first, as the GEMV
+// epilogue) for 9..32 activation rows. Library GEMMs take their fixed cost
+// per call at these sizes (a 32-row qkv projection in 12 us, 0.85 TB/s of
+// weights); this kernel streams each weight byte once at near the GEMV's
+// rate. Workgroup = 4 waves (8 for K = 6144) on one 16-row block of W (two
+// with SWI: gate and up) and every activation row; the waves split K in
+// slices, so a workgroup needs only 16 (32) weight rows and the grid has
+// N / 16 workgroups. Per 64-element K step a wave uses its W block (lane:
+// row l % 16, 16 bytes at k = 8 (l / 16) and 32 + 8 (l / 16): the A operands
+// of two v_mfma_f32_16x16x32_bf16), all of which it requests up front, and
+// the same k range of each 16-row activation block (B operands, from L2:
+// the rows are small and shared by all workgroups), 3 to 6 steps of which
+// are in flight. The slice sums are added in LDS in wave order, so the result
+// does not depend on timing.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <uint32_t MB, bool SWI, uint32_t KC>
+__global__ void __launch_bounds__(KC == 1u ? 256u : 512u)
+    gemm_rows_kernel(const uint16_t* w, const uint16_t* x, uint32_t ldx, uint16_t* y,
+                     uint32_t ldy, uint32_t M, uint32_t N) {
+    constexpr uint32_t WV = KC == 1u ? 4u : 8u;  // waves: K split in WV slices
+    constexpr uint32_t K = 2048u * KC, KW = K / WV, NS = KW / 64u;
+    constexpr uint32_t R = SWI ? 2u : 1u;
+    __shared__ f32x4_t red[WV][R][MB][64];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n0 = blockIdx.x * 16u;
+    const uint32_t r16 = lane & 15u, kq = 8u * (lane >> 4);
+    const uint32_t k0 = wave * KW + kq;
+    // The whole weight slice of the wave is requested first (NS * 2 loads
+    // per row block and lane): the small projections have few workgroups, and
+    // only all of a matrix in flight at once covers the memory latency.
+    uint4 wa[NS][R][2];
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r) {
+        const uint16_t* wr = w + (size_t)(n0 + r * N + r16) * K + k0;
+#pragma unroll
+        for (uint32_t st = 0; st < NS; ++st)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) wa[st][r][h] = ld16(wr + 64u * st + 32u * h);
+    }
+    // activation rows past M read row M - 1 (never stored); XD steps of them
+    // in flight (each step waits for one L2 round trip otherwise)
+    constexpr uint32_t XD0 = 96u / (8u * MB), XD = XD0 < NS ? XD0 : NS;
+    const uint16_t* xr[MB];
+#pragma unroll
+    for (uint32_t b = 0; b < MB; ++b) xr[b] = x + (size_t)min(16u * b + r16, M - 1u) * ldx + k0;
+    uint4 xb[XD][MB][2];
+    auto load_x = [&](uint32_t st, uint32_t slot) {
+#pragma unroll
+        for (uint32_t b = 0; b < MB; ++b)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) xb[slot][b][h] = ld16(xr[b] + 64u * st + 32u * h);
+    };
+#pragma unroll
+    for (uint32_t st = 0; st + 1u < XD; ++st) load_x(st, st);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4_t acc[R][MB];
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+        for (uint32_t b = 0; b < MB; ++b) acc[r][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t st = 0; st < NS; ++st) {
+        const uint32_t cur = st % XD;
+        if (st + XD - 1u < NS) load_x(st + XD - 1u, (st + XD - 1u) % XD);
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; ++h)
+#pragma unroll
+            for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+                for (uint32_t b = 0; b < MB; ++b)
+                    acc[r][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8_t, wa[st][r][h]),
+                        __builtin_bit_cast(bf16x8_t, xb[cur][b][h]), acc[r][b], 0, 0, 0);
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r)
+#pragma unroll
+        for (uint32_t b = 0; b < MB; ++b) red[wave][r][b][lane] = acc[r][b];
+    __syncthreads();
+    if (wave >= MB) return;  // wave b writes activation block b
+    const uint32_t b = wave;
+    const uint32_t m = 16u * b + r16;  // D layout: lane -> column m, rows 4 (l / 16) + j
+    f32x4_t t[R];
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r) {
+        t[r] = red[0][r][b][lane];
+#pragma unroll
+        for (uint32_t v = 1; v < WV; ++v) t[r] += red[v][r][b][lane];  // wave order
+    }
+    if (m >= M) return;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if constexpr (SWI) {
+            const float g = bf16_to_f32(f32_to_bf16(t[0][j]));
+            const float u = bf16_to_f32(f32_to_bf16(t[1][j]));
+            v[j] = silu_mul(g, u);
+        } else {
+            v[j] = t[0][j];
+        }
+    }
+    *reinterpret_cast<uint2*>(y + (size_t)m * ldy + n0 + 4u * (lane >> 4)) =
+        make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+}
+
+template <bool SWI, uint32_t KC>
+void launch_gemm_rows(const uint16_t* w, const uint16_t* x, uint32_t ldx, uint16_t* y,
+                      uint32_t ldy, uint32_t M, uint32_t N, hipStream_t st) {
+    const dim3 grid(N / 16u), block(KC == 1u ? 256u : 512u);
+    if (M <= 16u)
+        hipLaunchKernelGGL((gemm_rows_kernel<1, SWI, KC>), grid, block, 0, st, w, x, ldx, y, ldy,
+                           M, N);
+    else
+        hipLaunchKernelGGL((gemm_rows_kernel<2, SWI, KC>), grid, block, 0, st, w, x, ldx, y, ldy,
+                           M, N);
+}
+
 }  // namespace
 }  // namespace mckv
 
@@ -1058,4 +1180,28 @@ extern "C" mc_status_t mc_model_gemv_fp8_resnorm_swiglu(
     a.y = d_y;
     launch_gemv8<kProResnorm, 2, true>(a, (hipStream_t)stream);
     return check_launch("fp8 gemv (norm prologue, swiglu epilogue) launch failed");
+}
+
+extern "C" mc_status_t mc_model_gemm_rows(const uint16_t* d_w, const uint16_t* d_x, uint32_t ldx,
+                                          uint16_t* d_y, uint32_t ldy, uint32_t M, uint32_t N,
+                                          uint32_t K, uint32_t swiglu, void* stream) {
+    TraceRange trace_range("mc_model_gemm_rows");
+    if (d_w == nullptr || d_x == nullptr || d_y == nullptr || M < MC_MODEL_GEMM_ROWS_MIN ||
+        M > MC_MODEL_GEMM_ROWS_MAX || N == 0u || N % 16u != 0u || (K != 2048u && K != 6144u) ||
+        swiglu > 1u || (swiglu && K != 2048u) || ldx < K || ldy < N || ldx % 8u != 0u ||
+        ldy % 4u != 0u) {
+        set_error("mc_model_gemm_rows: invalid args (M=%u N=%u K=%u ldx=%u ldy=%u swiglu=%u; M "
+                  "%u..%u, N a multiple of 16, K 2048 or 6144 (2048 with swiglu), ldx a "
+                  "multiple of 8 and ldy of 4)",
+                  M, N, K, ldx, ldy, swiglu, MC_MODEL_GEMM_ROWS_MIN, MC_MODEL_GEMM_ROWS_MAX);
+        return MC_E_INVALID_ARGUMENT;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    if (swiglu) {
+        launch_gemm_rows<true, 1>(d_w, d_x, ldx, d_y, ldy, M, N, st);
+    } else {
+        if (K == 2048u) launch_gemm_rows<false, 1>(d_w, d_x, ldx, d_y, ldy, M, N, st);
+        else launch_gemm_rows<false, 3>(d_w, d_x, ldx, d_y, ldy, M, N, st);
+    }
+    return check_launch("row GEMM launch failed");
 }

@@ -72,6 +72,53 @@ def test_gemv(lib, orc, dev, M, N, K):
     assert np.all(got[:, N:] == np.uint16(0xFFFF))  # past N untouched
 
 
+@pytest.mark.parametrize("M,N,K,swi", [(9, 2560, 2048, 0), (16, 2048, 6144, 0),
+                                      (17, 2560, 2048, 0), (32, 2048, 2048, 0),
+                                      (25, 2048, 6144, 0), (32, 12288, 2048, 0),
+                                      (12, 6144, 2048, 1), (20, 6144, 2048, 1),
+                                      (32, 160, 2048, 1), (31, 96, 2048, 1)])
+def test_gemm_rows(lib, orc, dev, M, N, K, swi):
+    """Row GEMM of 9..32 rows (mc_model_gemm_rows) against a float64
+    product: plain, within 1 bf16 ulp for 99.9% of outputs (2 for all); with
+    the SwiGLU epilogue, the gate and up projections rounded to bf16 and then
+    the SwiGLU, within 2 ulps for 98%. Row strides past the matrices and the
+    output columns past N stay untouched."""
+    import torch
+    from oracle import model_ref as R
+    rng = np.random.default_rng(M * 131 + N + K + swi)
+    rows = 2 * N if swi else N
+    w = rnd_bf16(orc, rng, (rows, K), K ** -0.5)
+    x = rnd_bf16(orc, rng, (M, K + 16))  # row stride K + 16
+    y = torch.full((M, N + 4), -1, dtype=torch.int16, device=dev)
+    assert lib.mc_model_gemm_rows(P(to_dev(w, dev)), P(to_dev(x, dev)), K + 16, P(y), N + 4, M,
+                                  N, K, swi, stream()) == 0
+    torch.cuda.synchronize()
+    got = from_dev(y).reshape(M, N + 4)
+    prod = orc.bf16_to_f32(x[:, :K]).astype(np.float64) @ orc.bf16_to_f32(w).astype(np.float64).T
+    if swi:
+        gu = R.bf16(prod)
+        ref = R.silu_mul(gu[:, :N], gu[:, N:]).astype(np.float64)
+        ok, st = within_ulp(orc, got[:, :N], ref, ulps=2.0, frac=0.98)
+    else:
+        ok, st = within_ulp(orc, got[:, :N], prod)
+    assert ok, st
+    assert np.all(got[:, N:] == np.uint16(0xFFFF))
+
+
+def test_gemm_rows_rejects_bad_shapes(lib, dev):
+    """Row counts outside 9..32, N not a multiple of 16, K other than 2048 or
+    6144 (2048 with the SwiGLU epilogue), swiglu other than 0/1 and short
+    strides are MC_E_INVALID_ARGUMENT, with nothing launched."""
+    import torch
+    buf = torch.zeros(1 << 20, dtype=torch.int16, device=dev)
+    p = P(buf)
+    for M, N, K, ldx, ldy, swi in [(8, 2048, 2048, 2048, 2048, 0), (33, 2048, 2048, 2048, 2048, 0),
+                                   (32, 2050, 2048, 2048, 2050, 0), (32, 2048, 4096, 4096, 2048, 0),
+                                   (32, 2048, 2048, 2040, 2048, 0), (32, 2048, 2048, 2048, 2000, 0),
+                                   (32, 2048, 6144, 6144, 2048, 1), (32, 2048, 2048, 2048, 2048, 2)]:
+        assert lib.mc_model_gemm_rows(p, p, ldx, p, ldy, M, N, K, swi, stream()) == 1, (M, N, K)
+
+
 @pytest.mark.parametrize("M,add,N", [(1, False, 2560), (1, True, 2560), (4, True, 12288),
                                      (8, True, 1000)])
 def test_gemv_resnorm(lib, orc, dev, M, add, N):
@@ -633,20 +680,22 @@ m.close()
 
 
 def test_model_short_prefill_rows_path(rt, orc, model_dir, tmp_path):
-    """Prefill chunks of 2..16 tokens run their projections as GEMVs over
-    groups of up to 8 rows (forward_prefill_rows). Their last-row logits
-    match the oracle's forward, the greedy continuation matches the oracle's
-    decode, and they agree with the GEMM path (MC_PREFILL_ROWS_GEMV_OFF=1,
-    read once, so in a child process) to the logits tolerance. A prompt
-    prefilled as a 20-token call (GEMM path) and a 5-token call (row path)
-    gives the same logits on two sessions and matches the oracle."""
+    """Prefill chunks of 2..8 tokens run their projections as M-row GEMVs
+    (forward_prefill_rows), chunks of 9..32 tokens through the row GEMM
+    (mc_model_gemm_rows). Their last-row logits match the oracle's forward,
+    the greedy continuation matches the oracle's decode, and they agree with
+    the library GEMM path (MC_PREFILL_ROWS_GEMV_OFF=1, read once, so in a
+    child process) to the logits tolerance. A prompt prefilled as a 20-token
+    call (row GEMM) and a 5-token call (row GEMVs) gives the same logits on
+    two sessions and matches the oracle."""
     import json
     import subprocess
     import sys
     from oracle import model_ref as R
     path, w = model_dir
     prompts = [[7, 130000], [1, 500, 130559, 77, 9], [11 * i + 3 for i in range(8)],
-               [(13 * i + 5) % 130560 for i in range(13)], [17 * i for i in range(16)]]
+               [(13 * i + 5) % 130560 for i in range(13)], [17 * i for i in range(16)],
+               [(29 * i + 1) % 130560 for i in range(25)], [(7 * i) % 997 for i in range(32)]]
     m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2))
     s = rt.Session(m)
     got = []
@@ -680,8 +729,7 @@ def test_model_short_prefill_rows_path(rt, orc, model_dir, tmp_path):
         rel, cos = compare_logits(got[i], gemm[i])
         print(len(p), "rows: GEMM path rel", rel, "cos", cos)
         assert rel < 2e-2 and cos > 0.999, (len(p), rel, cos)
-    # a 5-token call after a 20-token one (GEMM path) continues the same session
-    # state
+    # a 5-token call after a 20-token one continues the same session state
     a, b = rt.Session(m), rt.Session(m)
     long_p = [(i * 7919 + 1) % 130560 for i in range(25)]
     a.prefill(long_p[:20])
