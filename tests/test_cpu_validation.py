@@ -156,3 +156,25 @@ def test_debug_hooks_without_handles(pkg, lib):
     assert b"both or neither" in lib.mc_last_error()
     assert lib.mc_kv_debug_decode_timeline(C.c_void_p(0x1000), 0) == INV
     assert lib.mc_kv_debug_decode_timeline(None, 0) == 0  # detach: no device needed
+
+
+def test_weight_path_kernels_reject(pkg, lib):
+    """The GEMV and row-GEMM entry points check rows, shapes and strides
+    before any device work."""
+    F = FAKE
+    # mc_model_gemv: M 1..8, K 2048 or 6144, strides
+    assert lib.mc_model_gemv(F, F, 2048, F, 2048, 0, 2048, 2048, None) == INV
+    assert lib.mc_model_gemv(F, F, 2048, F, 2048, 9, 2048, 2048, None) == INV
+    assert lib.mc_model_gemv(F, F, 4096, F, 2048, 1, 2048, 4096, None) == INV
+    assert lib.mc_model_gemv(F, F, 2000, F, 2048, 1, 2048, 2048, None) == INV
+    assert lib.mc_model_gemv(None, F, 2048, F, 2048, 1, 2048, 2048, None) == INV
+    # mc_model_gemm_rows: M 9..32, N % 16, K 2048 / 6144 (2048 with swiglu),
+    # swiglu 0/1, strides
+    good = [F, F, 2048, F, 2048, 20, 2048, 2048, 0, None]
+    for i, v in [(5, 8), (5, 33), (6, 2050), (7, 4096), (2, 2040), (4, 2000), (2, 2052),
+                 (8, 2), (0, None), (1, None), (3, None)]:
+        a = list(good)
+        a[i] = v
+        assert lib.mc_model_gemm_rows(*a) == INV, (i, v)
+        assert b"mc_model_gemm_rows" in lib.mc_last_error()
+    assert lib.mc_model_gemm_rows(F, F, 6144, F, 2048, 20, 2048, 6144, 1, None) == INV
