@@ -352,6 +352,7 @@ mc_status_t prefill_chunk(SessionImpl& s, uint32_t base, uint32_t n, bool first)
         // d_state.next_token, the token the first decode returns
         s.fwd.dump_step = s.debug_step;
         s.fwd.dump_layers = first;  // layer rows: the first chunk of the prefill
+        s.fwd.keys = base + n;
         const mc_status_t fs =
             forward_prefill(s.fwd, s.d_seq + base, n, &s.d_state->next_token);
         s.debug_step += 1;

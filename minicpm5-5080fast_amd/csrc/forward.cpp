@@ -432,6 +432,20 @@ void forward_carve(Forward& f, char* p, uint32_t rows, uint32_t logit_rows) {
     f.rows = rows;
 }
 
+// Key splits of a prefill chunk's attention: the reference's count for n
+// rows (kernels.h:517-521: 4096 / n, 1..8), capped so that each split gets
+// at least kSplitKeysMin keys of the chunk's last row. A split of a few
+// 64-key steps gains nothing and costs the merge kernel (a 32-token prompt:
+// 8 splits of 4 keys, attention 8.7 us + merge 5.0 us per layer). Splits
+// change the result's rounding only.
+constexpr uint32_t kSplitKeysMin = 512u;
+uint32_t prefill_splits(uint32_t n, uint32_t keys) {
+    const uint32_t s = mc_kv_prefill_split_kv(n);
+    if (keys == 0u) return s;
+    const uint32_t cap = keys / kSplitKeysMin;
+    return s < cap ? s : (cap < 1u ? 1u : cap);
+}
+
 // Projections of short prefill chunks (whole model, 42 layers, best of 5;
 // library GEMMs in parentheses): 2..8 tokens through forward_prefill_rows
 // 1.74-2.16 ms (3.60-3.67), 9..32 tokens through the row GEMM 2.45-3.31 ms
@@ -463,7 +477,7 @@ mc_status_t forward_prefill_rows(const Forward& f, const int32_t* d_ids, uint32_
     const uint16_t* pending = nullptr;
     const bool step_dump = dump_due(f.dump_step);
     const bool layer_dump = step_dump && f.dump_layers;
-    const uint32_t S = mc_kv_prefill_split_kv(n);
+    const uint32_t S = prefill_splits(n, f.keys);
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, cur, kHidden, n, st));
     for (uint32_t l = 0; l < kModelLayers; ++l) {
         if (layer_dump) {
@@ -538,7 +552,7 @@ mc_status_t forward_prefill(const Forward& f, const int32_t* d_ids, uint32_t n, 
     const uint16_t* res_last = res + (size_t)(n - 1u) * kHidden;
     FWD_OR_RETURN(mc_model_embedding_gather(w.embedding, d_ids, nullptr, res, kHidden, n, st));
     FWD_OR_RETURN(mc_model_rmsnorm_rows(res, nullptr, w.norm1[0], f.normed, n, kHidden, kRmsEps, st));
-    const uint32_t S = mc_kv_prefill_split_kv(n);
+    const uint32_t S = prefill_splits(n, f.keys);
     // 9..32 rows: the projections through the row GEMM (the gate_up one with
     // the SwiGLU as its epilogue), larger chunks through the GEMM libraries
     const bool rows = n >= MC_MODEL_GEMM_ROWS_MIN && n <= MC_MODEL_GEMM_ROWS_MAX &&

@@ -89,6 +89,9 @@ struct Forward {
     // forward and whether it may dump per-layer rows (the first prefill chunk)
     uint32_t dump_step = 0;
     bool dump_layers = false;
+    // prefill: positions the chunk's last row attends (base + n; 0 = not
+    // known), which caps the prefill attention's key splits
+    uint32_t keys = 0;
 };
 
 // Debug dump of the reference (debug_dump.h:1-12): with MC_DEBUG_DUMP_DIR set
