@@ -9,7 +9,7 @@ the headline workload C4 (one session, 131072 cached tokens in 2048 pages of
 second over the whole timed region (inputs resident in HBM); the other
 configurations are reported under "configs".
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,c5,pf,alloc,model,mprefill]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c4,c3,c1,c2,c5,pf,alloc,model,mprefill,rows]
 """
 from __future__ import annotations
 
@@ -690,6 +690,46 @@ def bench_model(pkg, torch, steps):
     }
 
 
+def bench_gemm_rows(pkg, torch, dev, reps):
+    """Row GEMM (mc_model_gemm_rows) of the four projections at 9, 16 and 32
+    activation rows: us per launch (HIP events over `reps` launches, weights
+    rotated over copies filling 512 MB so they come from HBM) and the weight
+    bytes' rate."""
+    lib = pkg._native.lib()
+    shapes = [("qkv", 2560, 2048, 0), ("o", 2048, 2048, 0), ("gate_up_swiglu", 6144, 2048, 1),
+              ("down", 2048, 6144, 0)]
+    out = {}
+    for M in (9, 16, 32):
+        row = {}
+        for name, N, K, swi in shapes:
+            rows = 2 * N if swi else N
+            copies = max(2, (512 << 20) // (rows * K * 2))
+            ws = [torch.randn(rows, K, device=dev).to(torch.bfloat16) for _ in range(copies)]
+            x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+            y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+            st = torch.cuda.current_stream().cuda_stream
+
+            def run(i):
+                r = lib.mc_model_gemm_rows(ws[i % copies].data_ptr(), x.data_ptr(), K,
+                                           y.data_ptr(), N, M, N, K, swi, st)
+                assert r == 0, r
+            for i in range(5):
+                run(i)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps):
+                run(i)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            row[name] = {"us": us, "weight_gbs": rows * K * 2 / us / 1e3}
+            del ws
+        row["total_us"] = sum(v["us"] for v in row.values())
+        out[f"rows_{M}"] = row
+    return out
+
+
 def bench_alloc(kvm):
     """Host page allocator (reference kv_cache.cpp:8-91 semantics, shared-pool
     form): 8 sessions grown to 131072 tokens of 64-token pages in one pool,
@@ -775,6 +815,10 @@ def main():
         res["model_decode"] = bench_model(pkg, torch, max(8, args.steps))
         log(res["model_decode"])
         torch.cuda.empty_cache()
+    if "rows" in cfgs:
+        log("row GEMM of the projections at 9 / 16 / 32 rows ...")
+        res["gemm_rows"] = bench_gemm_rows(pkg, torch, dev, 100)
+        log(res["gemm_rows"])
     if "mprefill" in cfgs:
         log("whole model with weights: 8448-token prefill ...")
         res["model_prefill"] = bench_model_prefill(pkg, torch, max(1, min(args.steps, 10)))
