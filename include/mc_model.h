@@ -96,8 +96,8 @@ mc_status_t mc_model_gemv_swiglu(const uint16_t* d_w, const uint16_t* d_gate_up,
  * n and N + n of d_w ([2N][K]: gate rows, then up rows) dotted with x_m and
  * rounded to bf16 (the gate_up projection followed by the SwiGLU, as
  * mc_model_gemv_resnorm_swiglu). N a multiple of 16, K 2048 or 6144 (2048
- * with swiglu), row
- * strides ldx (multiple of 8) and ldy (multiple of 4) in elements. No
+ * with swiglu), row strides ldx (multiple of 8) and ldy (multiple of 4) in
+ * elements, d_w and d_x 16-byte and d_y 8-byte aligned. No
  * reference counterpart: the reference runs every multi-token chunk through
  * cuBLAS (forward.cpp:200-420); this replaces the library GEMM where its
  * per-call cost dominates. */

@@ -1189,10 +1189,11 @@ extern "C" mc_status_t mc_model_gemm_rows(const uint16_t* d_w, const uint16_t* d
     if (d_w == nullptr || d_x == nullptr || d_y == nullptr || M < MC_MODEL_GEMM_ROWS_MIN ||
         M > MC_MODEL_GEMM_ROWS_MAX || N == 0u || N % 16u != 0u || (K != 2048u && K != 6144u) ||
         swiglu > 1u || (swiglu && K != 2048u) || ldx < K || ldy < N || ldx % 8u != 0u ||
-        ldy % 4u != 0u) {
+        ldy % 4u != 0u || (reinterpret_cast<uintptr_t>(d_w) | reinterpret_cast<uintptr_t>(d_x)) % 16u ||
+        reinterpret_cast<uintptr_t>(d_y) % 8u) {
         set_error("mc_model_gemm_rows: invalid args (M=%u N=%u K=%u ldx=%u ldy=%u swiglu=%u; M "
                   "%u..%u, N a multiple of 16, K 2048 or 6144 (2048 with swiglu), ldx a "
-                  "multiple of 8 and ldy of 4)",
+                  "multiple of 8 and ldy of 4, w and x 16-byte and y 8-byte aligned)",
                   M, N, K, ldx, ldy, swiglu, MC_MODEL_GEMM_ROWS_MIN, MC_MODEL_GEMM_ROWS_MAX);
         return MC_E_INVALID_ARGUMENT;
     }

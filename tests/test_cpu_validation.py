@@ -178,3 +178,7 @@ def test_weight_path_kernels_reject(pkg, lib):
         assert lib.mc_model_gemm_rows(*a) == INV, (i, v)
         assert b"mc_model_gemm_rows" in lib.mc_last_error()
     assert lib.mc_model_gemm_rows(F, F, 6144, F, 2048, 20, 2048, 6144, 1, None) == INV
+    for i, v in [(0, F + 8), (1, F + 8), (3, F + 4)]:  # misaligned w, x, y
+        a = list(good)
+        a[i] = v
+        assert lib.mc_model_gemm_rows(*a) == INV, (i, v)
