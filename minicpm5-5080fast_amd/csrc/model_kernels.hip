@@ -785,10 +785,12 @@ bool launch_gemv_m(uint32_t M, const GemvArgs& a, hipStream_t st) {
 // ---- row GEMM for prefill chunks of MC_MODEL_GEMM_ROWS_MIN..MAX rows ----
 // y[m][n] = bf16(sum_k W[n][k] x[m][k]) (or, SWI, bf16(silu(g) * u) of the
 // gate row n and up row N + n, each rounded to bf16 first, as the GEMV
-// epilogue) for 9..32 activation rows. Library GEMMs take their fixed cost
-// per call at these sizes (a 32-row qkv projection in 12 us, 0.85 TB/s of
-// weights); this kernel streams each weight byte once at near the GEMV's
-// rate. Workgroup = 4 waves (8 for K = 6144) on one 16-row block of W (two
+// epilogue) for 9..32 activation rows. The library kernels stream the
+// weights slowly at these sizes (hipBLASLt: a 32-row qkv projection in
+// 12 us, 0.85 TB/s); this kernel reads each weight byte once, at 1.1-3.8
+// TB/s (3.3-5.3 us for qkv, 13-18 us for gate_up + SwiGLU at 9-32 rows).
+// Its activation reads grow with the rows, which bounds it above 32.
+// Workgroup = 4 waves (8 for K = 6144) on one 16-row block of W (two
 // with SWI: gate and up) and every activation row; the waves split K in
 // slices, so a workgroup needs only 16 (32) weight rows and the grid has
 // N / 16 workgroups. Per 64-element K step a wave uses its W block (lane:
