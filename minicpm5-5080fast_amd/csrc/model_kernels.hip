@@ -788,7 +788,7 @@ bool launch_gemv_m(uint32_t M, const GemvArgs& a, hipStream_t st) {
 // epilogue) for 9..32 activation rows. The library kernels stream the
 // weights slowly at these sizes (hipBLASLt: a 32-row qkv projection in
 // 12 us, 0.85 TB/s); this kernel reads each weight byte once, at 1.1-3.8
-// TB/s (3.3-5.3 us for qkv, 13-18 us for gate_up + SwiGLU at 9-32 rows).
+// TB/s (5.3-7.7 us for qkv, 13-18 us for gate_up + SwiGLU at 9-32 rows).
 // Its activation reads grow with the rows, which bounds it above 32.
 // Workgroup = 4 waves (8 for K = 6144) on one 16-row block of W (two
 // with SWI: gate and up) and every activation row; the waves split K in
