@@ -40,7 +40,9 @@ extern "C" __attribute__((visibility("default"))) int tune_prefill_gemm_run() {
     void* ws;
     CK(hipMalloc(&ws, ws_bytes));
     rocblas_set_workspace(h, ws, ws_bytes);
-    const int Ms[] = {16, 32, 64, 128, 256, 512, 1024, 2048, 3072, 4096, 5120, 6144, 7168, 8448};
+    // Chunks below 256 rows run the library's own row kernels (up to 32 rows)
+    // or hipBLASLt, so the tables start at 256 rows.
+    const int Ms[] = {256, 512, 1024, 2048, 3072, 4096, 5120, 6144, 7168, 8448};
     const int NK[][2] = {{2560, 2048}, {2048, 2048}, {12288, 2048}, {2048, 6144}};
     void *W, *X, *Y;
     CK(hipMalloc(&W, (size_t)12288 * 6144 * 2));
