@@ -682,10 +682,14 @@ m.close()
 def test_model_short_prefill_rows_path(rt, orc, model_dir, tmp_path):
     """Prefill chunks of 2..8 tokens run their projections as M-row GEMVs
     (forward_prefill_rows), chunks of 9..32 tokens through the row GEMM
-    (mc_model_gemm_rows). Their last-row logits match the oracle's forward,
+    (mc_model_gemm_rows), and a 48-token chunk through hipBLASLt (the library
+    path of 33..1023 rows). Their last-row logits match the oracle's forward,
     the greedy continuation matches the oracle's decode, and they agree with
     the library GEMM path (MC_PREFILL_ROWS_GEMV_OFF=1, read once, so in a
-    child process) to the logits tolerance. A prompt prefilled as a 20-token
+    child process) to the logits tolerance. The child imports no torch and so
+    runs /opt/rocm's rocBLAS / hipBLASLt, where this process runs PyTorch's;
+    the 48-token chunk differs between the two only in rounding. A prompt
+    prefilled as a 20-token
     call (row GEMM) and a 5-token call (row GEMVs) gives the same logits on
     two sessions and matches the oracle."""
     import json
@@ -695,7 +699,8 @@ def test_model_short_prefill_rows_path(rt, orc, model_dir, tmp_path):
     path, w = model_dir
     prompts = [[7, 130000], [1, 500, 130559, 77, 9], [11 * i + 3 for i in range(8)],
                [(13 * i + 5) % 130560 for i in range(13)], [17 * i for i in range(16)],
-               [(29 * i + 1) % 130560 for i in range(25)], [(7 * i) % 997 for i in range(32)]]
+               [(29 * i + 1) % 130560 for i in range(25)], [(7 * i) % 997 for i in range(32)],
+               [(41 * i + 9) % 130560 for i in range(48)]]
     m = rt.Model(path, rt.model_options(max_context_tokens=4096, max_sessions=2))
     s = rt.Session(m)
     got = []
